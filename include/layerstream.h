@@ -1,0 +1,217 @@
+/*
+ * layerstream_amd: MI355X (gfx950) speculative-decoding verify engine for Qwen2-architecture
+ * models with tied embeddings, behind a C ABI.
+ *
+ * The reference (themaker00001/layerstream) is a Rust crate with no FFI; each entry point
+ * below names the reference interface it replaces (file:line in that crate), with the same
+ * argument meaning and error behaviour: bad requests return an error code and set a
+ * thread-local message (ls_last_error), they never abort.
+ *
+ * Conventions: every function returns 0 on success and a negative LS_E* code on error unless
+ * its comment says otherwise. Handles are not thread-safe (one caller thread per model, as the
+ * reference's `&mut self`). Output buffers are caller-owned; no pointer is retained across
+ * calls except where stated (a memory source borrows its buffers for its whole life).
+ */
+#ifndef LAYERSTREAM_H
+#define LAYERSTREAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LS_OK 0
+#define LS_E_INVALID (-1) /* bad request or argument (the reference's Err(String)) */
+#define LS_E_FORMAT (-2)  /* malformed config, header or file */
+#define LS_E_IO (-3)      /* file read failure */
+#define LS_E_DEVICE (-4)  /* HIP runtime failure */
+#define LS_E_STATE (-5)   /* call out of order (provider schedule, model in use) */
+
+/* Last error message of this thread (empty if none). Valid until the next call. */
+const char* ls_last_error(void);
+/* Library version string. */
+const char* ls_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * Formats. WeightFormat (src/weights.rs:14-55): bits 16 = bf16; 8 or 4 = symmetric integers
+ * with one bf16 scale per `group` weights, the scales after the packed integers of each row.
+ * ------------------------------------------------------------------------------------- */
+typedef struct {
+    int32_t bits;  /* 16, 8 or 4 */
+    int32_t group; /* 0 for bf16; 16..256, a multiple of 16 */
+} ls_format;
+
+/* Config (src/weights.rs:57-156). */
+typedef struct {
+    ls_format format;       /* the seven layer matrices */
+    ls_format embed_format; /* the tied embedding table / output head */
+    int64_t hidden, inter, layers, heads, kv_heads, head_dim, vocab, max_pos;
+    float eps, rope_theta;
+} ls_config;
+
+/* WeightFormat::row_bytes (src/weights.rs:26-31). Returns the byte count. */
+size_t ls_row_bytes(ls_format f, size_t cols);
+/* WeightFormat::validate (src/weights.rs:34-47). */
+int ls_format_validate(ls_format f, const size_t* cols, size_t n_cols);
+/* Config::from_json (src/weights.rs:77-141), including the layerstream_quant key. */
+int ls_config_from_json(const char* config_json, ls_config* out);
+/* layer_layout_for (src/weights.rs:215-227): 12 (offset, length) pairs in slot order
+ * input_norm, down, gate, up, post_norm, k_b, k_w, o_w, q_b, q_w, v_b, v_w. Returns the block
+ * size in bytes (0 on error). */
+size_t ls_layer_layout(const ls_config* cfg, size_t ranges[24]);
+/* inject_quant (src/quant.rs:137-145). Writes NUL-terminated text to out (cap bytes);
+ * *out_len = length without the NUL. embed_bits == 0 shares the layers' format. */
+int ls_inject_quant(const char* config_json, int bits, int group, int embed_bits, int embed_group, char* out,
+                    size_t cap, size_t* out_len);
+
+/* ---------------------------------------------------------------------------------------
+ * Quantizer: quantize_row (src/quant.rs:79-104) and quantize_model (src/quant.rs:158-251).
+ * ------------------------------------------------------------------------------------- */
+/* One row: out receives ls_row_bytes(f, cols) bytes. err/norm may be NULL. */
+int ls_quantize_row(ls_format f, const float* row, size_t cols, int clip_search, uint8_t* out, double* err,
+                    double* norm);
+/* A whole in-memory bf16 model into a `.lsq` image (src/weights.rs:327-358 layout): header,
+ * layer blocks, embedding table, final norm. bf16_config_json is the model's config.json text.
+ * With out == NULL only *out_len is set. threads <= 0 uses every core. rel_rmse may be NULL. */
+int ls_quantize_model(const char* bf16_config_json, const uint8_t* bf16_layers, const uint8_t* bf16_embed,
+                      const uint8_t* final_norm_bf16, ls_format fmt, ls_format embed_fmt, int clip_search,
+                      int threads, uint8_t* out, size_t out_cap, size_t* out_len, double* rel_rmse);
+
+/* Synthetic Qwen2 weights for benchmarks and tests (no reference counterpart: the reference
+ * reads real checkpoints). SplitMix64(seed) counter stream -> Box-Muller N(0, std) -> bf16
+ * round-to-nearest-even for every matrix and the q/k/v biases; RMSNorm weights are
+ * 1 + N(0, std). Layer blocks in slot order. Sizes: layers = cfg.layers * block bytes,
+ * embed = vocab * hidden * 2, norm = hidden * 2. cfg must be bf16. */
+int ls_synth_bf16_model(const ls_config* cfg, uint64_t seed, float std_dev, uint8_t* layers, uint8_t* embed,
+                        uint8_t* final_norm, int threads);
+
+/* ---------------------------------------------------------------------------------------
+ * Sources: trait Source (src/source.rs:23-33).
+ * ------------------------------------------------------------------------------------- */
+typedef struct ls_source ls_source;
+
+/* Borrowed in-memory model parts (the caller keeps them alive until ls_source_free):
+ * cfg.layers consecutive layer blocks, the embedding table, the bf16 final norm. */
+int ls_source_from_memory(const char* config_json, const uint8_t* layers, size_t layers_len,
+                          const uint8_t* embed, size_t embed_len, const uint8_t* final_norm_bf16,
+                          size_t norm_len, ls_source** out);
+/* ModelFiles::open_quantized + FileSource (src/weights.rs:389-424, src/source.rs:90-182):
+ * a `.lsq` file read with positioned reads. */
+int ls_source_open_lsq(const char* path, ls_source** out);
+/* A `.lsq` image already in memory (borrowed), with the same checks as the file. */
+int ls_source_from_lsq_image(const uint8_t* image, size_t len, ls_source** out);
+/* A copy of src's layers and embedding table in pinned host memory (hipHostMalloc), for the
+ * streaming mode's direct host -> device DMA ("pinned host buffers"). src may be freed after. */
+int ls_source_pinned_copy(const ls_source* src, ls_source** out);
+void ls_source_free(ls_source* s);
+int ls_source_config(const ls_source* s, ls_config* out);
+/* IoStats::bytes_read (src/source.rs:13-21). */
+uint64_t ls_source_bytes_read(const ls_source* s);
+
+/* ---------------------------------------------------------------------------------------
+ * Model (src/model.rs:16-140) on one MI355X. The provider decides where weights live
+ * (src/provider.rs:39-55): RESIDENT keeps every layer in HBM (ResidentProvider :61-137);
+ * STREAM keeps `slots` device layer slots fed from pinned host staging buffers by
+ * hipMemcpyAsync on a side stream, in the fixed schedule order layer 0..L-1 then the head
+ * chunks (StreamProvider :161-352).
+ * ------------------------------------------------------------------------------------- */
+typedef struct ls_model ls_model;
+
+#define LS_MODE_RESIDENT 0
+#define LS_MODE_STREAM 1
+
+/* Model::new (src/model.rs:58-77). The source must outlive the model. device = HIP device
+ * ordinal. */
+int ls_model_create(ls_source* src, int mode, int slots, size_t max_ctx, int device, ls_model** out);
+void ls_model_free(ls_model* m);
+/* Model::{pos, max_ctx, reset} (src/model.rs:84-103). */
+size_t ls_model_pos(const ls_model* m);
+size_t ls_model_max_ctx(const ls_model* m);
+void ls_model_reset(ls_model* m);
+/* Model::truncate (src/model.rs:137-140): forget cached tokens after pos. The reference asserts
+ * pos <= cached; here that is LS_E_INVALID. O(1): rejected K/V rows are overwritten later. */
+int ls_model_truncate(ls_model* m, size_t pos);
+/* Model::forward (src/model.rs:111-119): push tokens in 128-token chunks and return the
+ * logits of the last one. logits (vocab floats) and argmax may each be NULL. */
+int ls_model_forward(ls_model* m, const uint32_t* tokens, size_t n, float* logits, uint32_t* argmax);
+/* Model::forward_multi (src/model.rs:124-133): one weight pass over n <= 128 tokens, logits at
+ * the last n_logits positions (n_logits * vocab floats, may be NULL) and their argmax (first
+ * index of the maximum, src/spec.rs:41-49; may be NULL). */
+int ls_model_forward_multi(ls_model* m, const uint32_t* tokens, size_t n, size_t n_logits, float* logits,
+                           uint32_t* argmax);
+/* One greedy verify step of speculative decoding, fused on the device: forward_multi over
+ * block[0..n) with n = kk + 1 (block = [a, d_1 .. d_kk]), the per-position argmax, the
+ * longest-prefix acceptance of src/spec.rs:119-127 and the rollback truncate(p + m + 1) of
+ * src/spec.rs:137-139. Only *accepted (m) and *next (the correction or bonus token) return
+ * to the host. */
+int ls_model_verify_greedy(ls_model* m, const uint32_t* block, size_t n, uint32_t* accepted, uint32_t* next);
+
+/* Provider report (src/provider.rs:29-37). */
+typedef struct {
+    uint64_t resident_weight_bytes; /* device bytes held for weights */
+    uint64_t bytes_read;            /* source bytes read so far */
+    uint64_t wait_ns;               /* host time blocked waiting for streamed weights */
+    uint64_t h2d_bytes;             /* bytes copied host -> device for streamed weights */
+} ls_report;
+int ls_model_report(const ls_model* m, ls_report* out);
+/* Time of the last verify step on the device (HIP events around its kernels), in ms. */
+double ls_model_last_step_ms(const ls_model* m);
+
+/* ---------------------------------------------------------------------------------------
+ * Speculative decoding: speculative_greedy (src/spec.rs:57-152).
+ * ------------------------------------------------------------------------------------- */
+typedef struct {
+    uint64_t target_passes, drafted, accepted, draft_forwards;
+    double target_secs, draft_secs, first_secs, decode_secs;
+} ls_spec_stats; /* SpecStats + SpecResult times (src/spec.rs:17-39) */
+
+/* Draft source. The reference's draft is a `Model` (src/spec.rs:59); here any proposer plugs in
+ * through two callbacks, and two built-ins are provided. */
+typedef struct {
+    void* ctx;
+    /* Consume the prompt (src/spec.rs:84). */
+    int (*prefill)(void* ctx, const uint32_t* prompt, size_t n);
+    /* Propose kk tokens after `last` (src/spec.rs:100-107). Returns the forward calls made
+     * (>= 0) or a negative error. */
+    int (*propose)(void* ctx, uint32_t last, size_t kk, uint32_t* out);
+    /* After a pass that accepted m drafts, the target consumed block[0..m] (positions p..p+m);
+     * bring the draft to the same state (src/spec.rs:137-147). Returns forward calls made. */
+    int (*commit)(void* ctx, const uint32_t* block, size_t p, size_t m);
+} ls_drafter;
+
+/* A draft model on the device, exactly as the reference uses one. */
+int ls_drafter_from_model(ls_model* draft, ls_drafter* out);
+/* A scripted proposer for benchmarks: for output index i it proposes greedy[i] with
+ * probability p_accept, else a uniformly random other token (SplitMix64 counter stream keyed by
+ * seed and i). The returned drafter owns a copy of greedy; free it with ls_drafter_free. */
+int ls_drafter_scripted(const uint32_t* greedy, size_t n_greedy, double p_accept, uint64_t seed, uint64_t vocab,
+                        ls_drafter* out);
+/* The scripted proposal for output index i (for tests). */
+uint32_t ls_drafter_scripted_token(const ls_drafter* d, size_t i);
+void ls_drafter_free(ls_drafter* d);
+
+/* speculative_greedy (src/spec.rs:57-152). out receives up to max_new tokens; *out_len the
+ * count. Errors as the reference (:65-80): 1 <= k <= 32, a prompt, max_new >= 1, an empty target
+ * cache, prompt + max_new + k <= max_ctx. */
+int ls_speculative_greedy(ls_model* target, ls_drafter* draft, const uint32_t* prompt, size_t n_prompt,
+                          size_t max_new, size_t k, const uint32_t* eos, size_t n_eos, uint32_t* out,
+                          size_t* out_len, ls_spec_stats* stats);
+/* Plain greedy decoding with Sampler::greedy (src/model.rs:328-336), the parity baseline of
+ * tests/spec.rs:44-57. */
+int ls_greedy_generate(ls_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const uint32_t* eos,
+                       size_t n_eos, uint32_t* out, size_t* out_len);
+
+/* ---------------------------------------------------------------------------------------
+ * Operator level: kernels::matmul (src/kernels.rs:196-203) on device buffers.
+ * w_dev: the reference's row layout (rows * row_bytes); x_dev: t * cols f32; y_dev: t * rows
+ * f32. stream: a hipStream_t (NULL = default stream). Synchronous on that stream.
+ * ------------------------------------------------------------------------------------- */
+int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const float* x_dev, size_t t,
+              float* y_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

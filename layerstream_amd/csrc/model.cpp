@@ -1,0 +1,620 @@
+// The device Model (src/model.rs) and its providers (src/provider.rs) on one MI355X.
+//
+// HBM layout: per layer one arena holding the fused q|k|v matrix, o, the fused gate|up matrix
+// and down in the strip layout (kernels.hpp), then the q|k|v bias and the two RMSNorm weight
+// vectors as f32. The tied embedding table is one strip-layout matrix used both for the
+// embedding gather and as the output head. The KV cache is f32 [layer][max_ctx][kv_dim] for K
+// and for V, as the reference's (src/model.rs:67-68); rollback is O(1) (only `pos` moves).
+#include "model.hpp"
+
+#include <chrono>
+#include <cmath>
+
+namespace ls {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw Error(LS_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+DevBuf::DevBuf(size_t bytes) : n(bytes) {
+    if (bytes) HIPC(hipMalloc(&p, bytes));
+}
+DevBuf::~DevBuf() {
+    if (p) (void)hipFree(p);
+}
+DevBuf& DevBuf::operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+        if (p) (void)hipFree(p);
+        p = o.p;
+        n = o.n;
+        o.p = nullptr;
+        o.n = 0;
+    }
+    return *this;
+}
+
+PinnedBuf::PinnedBuf(size_t bytes) : n(bytes) {
+    if (bytes) HIPC(hipHostMalloc(&p, bytes, hipHostMallocDefault));
+}
+PinnedBuf::~PinnedBuf() {
+    if (p) (void)hipHostFree(p);
+}
+PinnedBuf& PinnedBuf::operator=(PinnedBuf&& o) noexcept {
+    if (this != &o) {
+        if (p) (void)hipHostFree(p);
+        p = o.p;
+        n = o.n;
+        o.p = nullptr;
+        o.n = 0;
+    }
+    return *this;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+DevMat bind_mat(uint8_t* data, uint16_t* scales, const Format& f, int rows, int cols) {
+    DevMat m;
+    m.data = data;
+    m.scales = f.is_bf16() ? nullptr : scales;
+    m.bits = f.bits;
+    m.group = f.is_bf16() ? 0 : f.group;
+    m.rows = rows;
+    m.cols = cols;
+    m.n_strips = (rows + STRIP - 1) / STRIP;
+    m.n_chunks = devmat_chunks(f.bits, cols);
+    m.n_groups = f.is_bf16() ? 0 : cols / f.group;
+    return m;
+}
+
+static void mat_region(size_t& off, size_t& d, size_t& s, const Format& f, size_t rows, size_t cols) {
+    d = off;
+    off = align256(off + devmat_data_bytes(f.bits, int(rows), int(cols)));
+    s = off;
+    off = align256(off + 2 * devmat_scale_count(f.bits, f.group, int(rows), int(cols)));
+}
+
+LayerArena layer_arena(const Config& c) {
+    LayerArena a{};
+    size_t off = 0, h = c.hidden, kv = c.kv_dim(), in = c.inter;
+    mat_region(off, a.qkv_d, a.qkv_s, c.format, h + 2 * kv, h);
+    mat_region(off, a.o_d, a.o_s, c.format, h, h);
+    mat_region(off, a.gu_d, a.gu_s, c.format, 2 * in, h);
+    mat_region(off, a.down_d, a.down_s, c.format, h, in);
+    a.b_qkv = off;
+    off = align256(off + 4 * (h + 2 * kv));
+    a.in_norm = off;
+    off = align256(off + 4 * h);
+    a.post_norm = off;
+    off = align256(off + 4 * h);
+    a.total = off;
+    return a;
+}
+
+DevLayer bind_layer(const Config& c, const LayerArena& a, uint8_t* b) {
+    DevLayer L;
+    int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter);
+    L.qkv = bind_mat(b + a.qkv_d, reinterpret_cast<uint16_t*>(b + a.qkv_s), c.format, h + 2 * kv, h);
+    L.o = bind_mat(b + a.o_d, reinterpret_cast<uint16_t*>(b + a.o_s), c.format, h, h);
+    L.gu = bind_mat(b + a.gu_d, reinterpret_cast<uint16_t*>(b + a.gu_s), c.format, 2 * in, h);
+    L.down = bind_mat(b + a.down_d, reinterpret_cast<uint16_t*>(b + a.down_s), c.format, h, in);
+    L.b_qkv = reinterpret_cast<const float*>(b + a.b_qkv);
+    L.in_norm = reinterpret_cast<const float*>(b + a.in_norm);
+    L.post_norm = reinterpret_cast<const float*>(b + a.post_norm);
+    return L;
+}
+
+// Fill the padding of every matrix of an arena: int4 padding bytes must decode to weight 0.
+static void init_arena(const Config& c, const LayerArena& a, uint8_t* b, hipStream_t s) {
+    HIPC(hipMemsetAsync(b, 0, a.total, s));
+    if (c.format.bits == 4) {
+        size_t h = c.hidden, kv = c.kv_dim(), in = c.inter;
+        HIPC(hipMemsetAsync(b + a.qkv_d, 0x88, devmat_data_bytes(4, int(h + 2 * kv), int(h)), s));
+        HIPC(hipMemsetAsync(b + a.o_d, 0x88, devmat_data_bytes(4, int(h), int(h)), s));
+        HIPC(hipMemsetAsync(b + a.gu_d, 0x88, devmat_data_bytes(4, int(2 * in), int(h)), s));
+        HIPC(hipMemsetAsync(b + a.down_d, 0x88, devmat_data_bytes(4, int(h), int(in)), s));
+    }
+}
+
+void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* raw, const LayerArena& a, uint8_t* b,
+                        hipStream_t s) {
+    const int bits = c.format.bits, g = c.format.group;
+    const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter);
+    auto rp = [&](int slot, int rows, int cols, size_t d, size_t sc, int row_off) {
+        repack_rows_device(raw + L.off[slot], bits, g, rows, cols, b + d, reinterpret_cast<uint16_t*>(b + sc), row_off, 0, s);
+    };
+    rp(T_Q_W, h, h, a.qkv_d, a.qkv_s, 0);
+    rp(T_K_W, kv, h, a.qkv_d, a.qkv_s, h);
+    rp(T_V_W, kv, h, a.qkv_d, a.qkv_s, h + kv);
+    rp(T_O_W, h, h, a.o_d, a.o_s, 0);
+    rp(T_GATE, in, h, a.gu_d, a.gu_s, 0);
+    rp(T_UP, in, h, a.gu_d, a.gu_s, in);
+    rp(T_DOWN, h, in, a.down_d, a.down_s, 0);
+    float* bq = reinterpret_cast<float*>(b + a.b_qkv);
+    bf16_to_f32_dev(raw + L.off[T_Q_B], h, bq, s);
+    bf16_to_f32_dev(raw + L.off[T_K_B], kv, bq + h, s);
+    bf16_to_f32_dev(raw + L.off[T_V_B], kv, bq + h + kv, s);
+    bf16_to_f32_dev(raw + L.off[T_INPUT_NORM], h, reinterpret_cast<float*>(b + a.in_norm), s);
+    bf16_to_f32_dev(raw + L.off[T_POST_NORM], h, reinterpret_cast<float*>(b + a.post_norm), s);
+}
+
+// ---------------------------------------------------------------------------------------
+// Resident: every layer and the whole table in HBM (ResidentProvider, src/provider.rs:61-137)
+// ---------------------------------------------------------------------------------------
+class ResidentProvider : public DeviceProvider {
+public:
+    ResidentProvider(const Source& src, hipStream_t s) : src_(src), c_(src.cfg()), a_(layer_arena(c_)), s_(s) {
+        const LayerLayout L = src.layout();
+        arena_ = DevBuf(a_.total * c_.layers);
+        const size_t rb = c_.row_bytes();
+        const size_t stage_bytes = std::max(L.total, HEAD_ROWS * rb);
+        PinnedBuf stage(stage_bytes);
+        DevBuf raw(stage_bytes);
+        for (size_t l = 0; l < c_.layers; l++) {
+            uint8_t* b = arena_.as<uint8_t>() + l * a_.total;
+            init_arena(c_, a_, b, s_);
+            src.read_layer(l, stage.as<uint8_t>());
+            HIPC(hipMemcpyAsync(raw.p, stage.p, L.total, hipMemcpyHostToDevice, s_));
+            build_layer_device(c_, L, raw.as<uint8_t>(), a_, b, s_);
+            HIPC(hipStreamSynchronize(s_));
+            layers_.push_back(bind_layer(c_, a_, b));
+        }
+        const Format ef = c_.embed_format;
+        const int V = int(c_.vocab), h = int(c_.hidden);
+        edata_ = DevBuf(devmat_data_bytes(ef.bits, V, h));
+        escales_ = DevBuf(std::max<size_t>(2, 2 * devmat_scale_count(ef.bits, ef.group, V, h)));
+        HIPC(hipMemsetAsync(edata_.p, ef.bits == 4 ? 0x88 : 0, edata_.n, s_));
+        HIPC(hipMemsetAsync(escales_.p, 0, escales_.n, s_));
+        for (size_t first = 0; first < c_.vocab; first += HEAD_ROWS) {
+            size_t rows = std::min(HEAD_ROWS, c_.vocab - first);
+            src.read_embed_rows(first, rows, stage.as<uint8_t>());
+            HIPC(hipMemcpyAsync(raw.p, stage.p, rows * rb, hipMemcpyHostToDevice, s_));
+            repack_rows_device(raw.as<uint8_t>(), ef.bits, ef.group, int(rows), h, edata_.as<uint8_t>(), escales_.as<uint16_t>(),
+                               int(first), V, s_);
+            HIPC(hipStreamSynchronize(s_));
+        }
+        E_ = bind_mat(edata_.as<uint8_t>(), escales_.as<uint16_t>(), ef, V, h);
+        head_splits = matvec_splits(E_, 1);
+    }
+    const char* name() const override { return "resident"; }
+    void begin_forward(bool) override {}
+    const DevLayer& layer(size_t l) override {
+        if (l >= layers_.size()) fail("layer " + std::to_string(l) + " out of range");
+        return layers_[l];
+    }
+    void release_layer(size_t) override {}
+    size_t n_head_chunks() const override { return 1; }
+    HeadChunk head_chunk(size_t c) override {
+        if (c != 0) fail("head chunk out of range");
+        return HeadChunk{0, c_.vocab, E_};
+    }
+    void release_head_chunk(size_t) override {}
+    void end_forward() override {}
+    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x) override { embed_gather(E_, dev_tokens, t, x, s_); }
+    ls_report report() const override {
+        ls_report r{};
+        r.resident_weight_bytes = arena_.n + edata_.n + escales_.n;
+        r.bytes_read = src_.bytes_read();
+        return r;
+    }
+
+private:
+    const Source& src_;
+    Config c_;
+    LayerArena a_;
+    hipStream_t s_;
+    DevBuf arena_, edata_, escales_;
+    std::vector<DevLayer> layers_;
+    DevMat E_;
+};
+
+// ---------------------------------------------------------------------------------------
+// Streaming: `slots` device slots fed in schedule order (StreamProvider, src/provider.rs:161-352).
+// A slot holds the raw block (copied host -> device on a side stream), the arena it is
+// rearranged into, and events: `copied` (its host staging buffer may be refilled), `ready`
+// (the arena may be computed on) and `freed` (the compute stream is done with it). With a
+// pinned source the copy goes straight from the source's memory; otherwise the host reads
+// into a pinned staging buffer first.
+// ---------------------------------------------------------------------------------------
+class StreamProvider : public DeviceProvider {
+    enum Kind { LAYER, HEAD };
+    struct Item {
+        Kind kind;
+        size_t idx;
+        bool operator==(const Item& o) const { return kind == o.kind && idx == o.idx; }
+    };
+    struct Slot {
+        DevBuf raw, arena, hdata, hscales;
+        PinnedBuf stage;
+        hipEvent_t copied = nullptr, ready = nullptr, freed = nullptr;
+        bool used = false;
+    };
+
+public:
+    StreamProvider(const Source& src, int slots, hipStream_t compute)
+        : src_(src), c_(src.cfg()), L_(src.layout()), a_(layer_arena(c_)), compute_(compute) {
+        if (slots < 1) slots = 1;
+        HIPC(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking));
+        const size_t rb = c_.row_bytes();
+        buf_size_ = std::max(L_.total, std::min(HEAD_ROWS, c_.vocab) * rb);
+        const Format ef = c_.embed_format;
+        const int h = int(c_.hidden);
+        slots_.resize(size_t(slots));
+        for (auto& s : slots_) {
+            s.raw = DevBuf(buf_size_);
+            s.arena = DevBuf(a_.total);
+            init_arena(c_, a_, s.arena.as<uint8_t>(), copy_);
+            s.hdata = DevBuf(devmat_data_bytes(ef.bits, int(HEAD_ROWS), h));
+            s.hscales = DevBuf(std::max<size_t>(2, 2 * devmat_scale_count(ef.bits, ef.group, int(HEAD_ROWS), h)));
+            HIPC(hipMemsetAsync(s.hdata.p, ef.bits == 4 ? 0x88 : 0, s.hdata.n, copy_));
+            HIPC(hipMemsetAsync(s.hscales.p, 0, s.hscales.n, copy_));
+            if (!src_.pinned()) s.stage = PinnedBuf(buf_size_);
+            HIPC(hipEventCreateWithFlags(&s.copied, hipEventDisableTiming));
+            HIPC(hipEventCreateWithFlags(&s.ready, hipEventDisableTiming));
+            HIPC(hipEventCreateWithFlags(&s.freed, hipEventDisableTiming));
+        }
+        HIPC(hipStreamSynchronize(copy_));
+        // The head's K split is the one of the whole table, so logits match the resident mode.
+        DevMat full = bind_mat(nullptr, nullptr, ef, int(c_.vocab), h);
+        head_splits = matvec_splits(full, 1);
+        embed_stage_ = PinnedBuf(128 * rb);
+        embed_raw_ = DevBuf(128 * rb);
+        HIPC(hipEventCreateWithFlags(&embed_copied_, hipEventDisableTiming));
+    }
+    ~StreamProvider() override {
+        (void)hipStreamSynchronize(copy_);
+        (void)hipStreamSynchronize(compute_);
+        for (auto& s : slots_) {
+            (void)hipEventDestroy(s.copied);
+            (void)hipEventDestroy(s.ready);
+            (void)hipEventDestroy(s.freed);
+        }
+        (void)hipEventDestroy(embed_copied_);
+        (void)hipStreamDestroy(copy_);
+    }
+    const char* name() const override { return "stream"; }
+
+    void begin_forward(bool with_head) override {
+        // Recover from an earlier pass that stopped early: wait for copies in flight.
+        HIPC(hipStreamSynchronize(copy_));
+        schedule_.clear();
+        for (size_t l = 0; l < c_.layers; l++) schedule_.push_back({LAYER, l});
+        if (with_head)
+            for (size_t c = 0; c < n_head_chunks(); c++) schedule_.push_back({HEAD, c});
+        next_issue_ = next_take_ = 0;
+        holding_ = false;
+        while (next_issue_ < schedule_.size() && next_issue_ < slots_.size()) issue();
+    }
+
+    const DevLayer& layer(size_t l) override {
+        Slot& s = take({LAYER, l});
+        cur_layer_ = bind_layer(c_, a_, s.arena.as<uint8_t>());
+        return cur_layer_;
+    }
+    void release_layer(size_t) override { release(); }
+    size_t n_head_chunks() const override { return (c_.vocab + HEAD_ROWS - 1) / HEAD_ROWS; }
+    HeadChunk head_chunk(size_t c) override {
+        Slot& s = take({HEAD, c});
+        size_t first = c * HEAD_ROWS, rows = std::min(HEAD_ROWS, c_.vocab - first);
+        return HeadChunk{first, rows, bind_mat(s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>(), c_.embed_format, int(rows), int(c_.hidden))};
+    }
+    void release_head_chunk(size_t) override { release(); }
+    void end_forward() override {
+        if (holding_) release();
+        if (next_take_ != schedule_.size())
+            fail("forward pass ended before every scheduled item was consumed", LS_E_STATE);
+    }
+
+    void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x) override {
+        // Rows come from the source on every pass, as src/provider.rs:284-286.
+        const size_t rb = c_.row_bytes();
+        HIPC(hipEventSynchronize(embed_copied_));
+        for (int i = 0; i < t; i++) src_.read_embed_rows(host_tokens[i], 1, embed_stage_.as<uint8_t>() + size_t(i) * rb);
+        HIPC(hipMemcpyAsync(embed_raw_.p, embed_stage_.p, size_t(t) * rb, hipMemcpyHostToDevice, compute_));
+        HIPC(hipEventRecord(embed_copied_, compute_));
+        embed_raw_rows(embed_raw_.as<uint8_t>(), c_.embed_format.bits, c_.embed_format.group, int(c_.hidden), t, x, compute_);
+    }
+
+    ls_report report() const override {
+        ls_report r{};
+        r.resident_weight_bytes = 0;
+        for (auto& s : slots_) r.resident_weight_bytes += s.raw.n + s.arena.n + s.hdata.n + s.hscales.n;
+        r.bytes_read = src_.bytes_read();
+        r.wait_ns = wait_ns_;
+        r.h2d_bytes = h2d_bytes_;
+        return r;
+    }
+
+private:
+    void issue() {
+        const Item it = schedule_[next_issue_];
+        Slot& s = slots_[next_issue_ % slots_.size()];
+        const size_t rb = c_.row_bytes();
+        size_t bytes, first = 0, rows = 0;
+        if (it.kind == LAYER) {
+            bytes = L_.total;
+        } else {
+            first = it.idx * HEAD_ROWS;
+            rows = std::min(HEAD_ROWS, c_.vocab - first);
+            bytes = rows * rb;
+        }
+        const uint8_t* from;
+        if (src_.pinned()) {
+            from = it.kind == LAYER ? src_.layer_view(it.idx) : src_.embed_view() + first * rb;
+            src_.count_read(bytes);
+        } else {
+            auto t0 = std::chrono::steady_clock::now();
+            HIPC(hipEventSynchronize(s.copied));  // the staging buffer's previous copy has landed
+            wait_ns_ += uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count());
+            if (it.kind == LAYER) src_.read_layer(it.idx, s.stage.as<uint8_t>());
+            else src_.read_embed_rows(first, rows, s.stage.as<uint8_t>());
+            from = s.stage.as<uint8_t>();
+        }
+        if (s.used) HIPC(hipStreamWaitEvent(copy_, s.freed, 0));
+        HIPC(hipMemcpyAsync(s.raw.p, from, bytes, hipMemcpyHostToDevice, copy_));
+        h2d_bytes_ += bytes;
+        HIPC(hipEventRecord(s.copied, copy_));
+        if (it.kind == LAYER) {
+            build_layer_device(c_, L_, s.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), copy_);
+        } else {
+            const Format ef = c_.embed_format;
+            repack_rows_device(s.raw.as<uint8_t>(), ef.bits, ef.group, int(rows), int(c_.hidden), s.hdata.as<uint8_t>(),
+                               s.hscales.as<uint16_t>(), 0, int(HEAD_ROWS), copy_);
+        }
+        HIPC(hipEventRecord(s.ready, copy_));
+        s.used = true;
+        next_issue_++;
+    }
+
+    Slot& take(const Item& want) {
+        if (holding_) release();
+        if (next_take_ >= schedule_.size() || !(schedule_[next_take_] == want))
+            fail(std::string("provider asked for ") + (want.kind == LAYER ? "layer " : "head chunk ") + std::to_string(want.idx) +
+                     " out of schedule order",
+                 LS_E_STATE);
+        Slot& s = slots_[next_take_ % slots_.size()];
+        HIPC(hipStreamWaitEvent(compute_, s.ready, 0));
+        holding_ = true;
+        return s;
+    }
+
+    void release() {
+        if (!holding_) return;
+        Slot& s = slots_[next_take_ % slots_.size()];
+        HIPC(hipEventRecord(s.freed, compute_));
+        holding_ = false;
+        next_take_++;
+        while (next_issue_ < schedule_.size() && next_issue_ < next_take_ + slots_.size()) issue();
+    }
+
+    const Source& src_;
+    Config c_;
+    LayerLayout L_;
+    LayerArena a_;
+    hipStream_t compute_, copy_ = nullptr;
+    std::vector<Slot> slots_;
+    std::vector<Item> schedule_;
+    size_t next_issue_ = 0, next_take_ = 0, buf_size_ = 0;
+    bool holding_ = false;
+    DevLayer cur_layer_;
+    PinnedBuf embed_stage_;
+    DevBuf embed_raw_;
+    hipEvent_t embed_copied_ = nullptr;
+    uint64_t wait_ns_ = 0, h2d_bytes_ = 0;
+};
+
+std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t s) {
+    return std::make_unique<ResidentProvider>(src, s);
+}
+std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStream_t s) {
+    return std::make_unique<StreamProvider>(src, slots, s);
+}
+
+// ---------------------------------------------------------------------------------------
+// Model
+// ---------------------------------------------------------------------------------------
+constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
+
+Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
+    : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx) {
+    if (max_ctx == 0) fail("max_ctx must be positive");
+    const Config& c = cfg_;
+    if (c.embed_format.is_bf16() && c.hidden % 8 != 0) fail("bf16 rows must hold a multiple of 8 values");
+    if (c.format.is_bf16() && (c.hidden % 8 != 0 || c.inter % 8 != 0)) fail("bf16 rows must hold a multiple of 8 values");
+    if (c.head_dim > 256 || 256 % c.head_dim != 0) fail("head_dim must divide 256");
+    HIPC(hipSetDevice(device));
+    HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    HIPC(hipEventCreate(&ev0_));
+    HIPC(hipEventCreate(&ev1_));
+    if (mode == LS_MODE_RESIDENT) prov_ = make_resident(src, stream_);
+    else if (mode == LS_MODE_STREAM) prov_ = make_stream(src, slots, stream_);
+    else fail("unknown mode " + std::to_string(mode) + " (use resident or stream)");
+
+    const size_t h = c.hidden, kv = c.kv_dim(), in = c.inter, T = PREFILL_CHUNK;
+    kcache_ = DevBuf(c.layers * max_ctx * kv * 4);
+    vcache_ = DevBuf(c.layers * max_ctx * kv * 4);
+    HIPC(hipMemsetAsync(kcache_.p, 0, kcache_.n, stream_));
+    HIPC(hipMemsetAsync(vcache_.p, 0, vcache_.n, stream_));
+
+    // RoPE table on the host with glibc, as the reference computes each angle (src/model.rs:63-65,
+    // src/kernels.rs:246-247): inv_freq in f64 cast to f32, angle = (pos as f32) * inv_freq.
+    const size_t half = c.head_dim / 2;
+    std::vector<float> inv(half), cs(max_ctx * half), sn(max_ctx * half);
+    for (size_t i = 0; i < half; i++)
+        inv[i] = float(1.0 / std::pow(double(c.rope_theta), double(2 * i) / double(c.head_dim)));
+    for (size_t p = 0; p < max_ctx; p++)
+        for (size_t i = 0; i < half; i++) {
+            float ang = float(p) * inv[i];
+            cs[p * half + i] = cosf(ang);
+            sn[p * half + i] = sinf(ang);
+        }
+    rope_cos_ = DevBuf(cs.size() * 4);
+    rope_sin_ = DevBuf(sn.size() * 4);
+    HIPC(hipMemcpy(rope_cos_.p, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIPC(hipMemcpy(rope_sin_.p, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    fnorm_ = DevBuf(h * 4);
+    HIPC(hipMemcpy(fnorm_.p, src.final_norm().data(), h * 4, hipMemcpyHostToDevice));
+
+    // Split counts depend only on matrix shapes (so results never depend on t).
+    DevMat qkv = bind_mat(nullptr, nullptr, c.format, int(h + 2 * kv), int(h));
+    DevMat o = bind_mat(nullptr, nullptr, c.format, int(h), int(h));
+    DevMat gu = bind_mat(nullptr, nullptr, c.format, int(2 * in), int(h));
+    DevMat dn = bind_mat(nullptr, nullptr, c.format, int(h), int(in));
+    s_qkv_ = matvec_splits(qkv, 1);
+    s_o_ = matvec_splits(o, 1);
+    s_gu_ = matvec_splits(gu, 1);
+    s_down_ = matvec_splits(dn, 1);
+    auto rp = [](const DevMat& m) { return size_t(m.n_strips) * STRIP; };
+    vpad_ = (c.vocab + STRIP - 1) / STRIP * STRIP;
+    part_floats_ = std::max({s_qkv_ * rp(qkv), s_o_ * rp(o), s_gu_ * rp(gu), s_down_ * rp(dn),
+                             size_t(prov_->head_splits) * std::max(vpad_, HEAD_ROWS)}) * T;
+
+    x_ = DevBuf(T * h * 4);
+    xn_ = DevBuf(T * h * 4);
+    qkv_ = DevBuf(T * (h + 2 * kv) * 4);
+    attn_ = DevBuf(T * h * 4);
+    gu_ = DevBuf(T * 2 * in * 4);
+    act_ = DevBuf(T * in * 4);
+    part_ = DevBuf(part_floats_ * 4);
+    scores_ = DevBuf(T * c.heads * max_ctx * 4);
+    logits_ = DevBuf(T * vpad_ * 4);
+    hf_ = DevBuf(T * h * 4);
+    amax_ = DevBuf(T * 4);
+    pval_ = DevBuf(T * 64 * 4);
+    pidx_ = DevBuf(T * 64 * 4);
+    tok_ = DevBuf(T * 4);
+    acc_ = DevBuf(16);
+    h_tok_ = PinnedBuf(T * 4);
+    h_out_ = PinnedBuf(T * 4 + 16);
+    HIPC(hipStreamSynchronize(stream_));
+}
+
+Model::~Model() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    prov_.reset();
+    if (ev0_) (void)hipEventDestroy(ev0_);
+    if (ev1_) (void)hipEventDestroy(ev1_);
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Model::truncate(size_t pos) {
+    if (pos > pos_) fail("cannot truncate to " + std::to_string(pos) + ": only " + std::to_string(pos_) + " tokens are cached");
+    pos_ = pos;
+}
+
+void Model::check_request(const uint32_t* tok, size_t n) const {
+    if (n == 0) fail("no tokens to process");
+    if (!tok) fail("no token buffer");
+    if (pos_ + n > max_ctx_)
+        fail("context is full: " + std::to_string(pos_) + " cached + " + std::to_string(n) + " new tokens exceeds the limit of " +
+             std::to_string(max_ctx_));
+    for (size_t i = 0; i < n; i++)
+        if (tok[i] >= cfg_.vocab) fail("token id " + std::to_string(tok[i]) + " is outside the vocabulary");
+}
+
+// forward_chunk (src/model.rs:161-220), all on the compute stream.
+void Model::forward_chunk(const uint32_t* tok, size_t t, size_t n_logits) {
+    const Config& c = cfg_;
+    const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter), T = int(t);
+    const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim), pos0 = int(pos_);
+    hipStream_t s = stream_;
+    std::memcpy(h_tok_.p, tok, t * 4);
+    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, t * 4, hipMemcpyHostToDevice, s));
+    float* x = x_.as<float>();
+    float* xn = xn_.as<float>();
+    float* qkv = qkv_.as<float>();
+    float* part = part_.as<float>();
+    prov_->embed(tok, tok_.as<uint32_t>(), T, x);
+    prov_->begin_forward(n_logits > 0);
+    for (size_t l = 0; l < c.layers; l++) {
+        const DevLayer& L = prov_->layer(l);
+        float* kc = kcache_.as<float>() + l * max_ctx_ * kv;
+        float* vc = vcache_.as<float>() + l * max_ctx_ * kv;
+        rms_norm(x, L.in_norm, h, c.eps, T, xn, s);
+        matvec(L.qkv, xn, h, T, part, s_qkv_, s);
+        reduce_store(part, s_qkv_, T, h + 2 * kv, L.qkv.n_strips * STRIP, L.b_qkv, qkv, h + 2 * kv, s);
+        rope_append_kv(qkv, T, heads, kvh, hd, pos0, rope_cos_.as<float>(), rope_sin_.as<float>(), kc, vc, s);
+        attention(qkv, T, heads, kvh, hd, pos0, int(max_ctx_), kc, vc, scores_.as<float>(), attn_.as<float>(), s);
+        matvec(L.o, attn_.as<float>(), h, T, part, s_o_, s);
+        reduce_residual(part, s_o_, T, h, L.o.n_strips * STRIP, x, h, s);
+        rms_norm(x, L.post_norm, h, c.eps, T, xn, s);
+        matvec(L.gu, xn, h, T, part, s_gu_, s);
+        reduce_store(part, s_gu_, T, 2 * in, L.gu.n_strips * STRIP, nullptr, gu_.as<float>(), 2 * in, s);
+        silu_mul(gu_.as<float>(), T, in, act_.as<float>(), s);
+        matvec(L.down, act_.as<float>(), in, T, part, s_down_, s);
+        reduce_residual(part, s_down_, T, h, L.down.n_strips * STRIP, x, h, s);
+        prov_->release_layer(l);
+    }
+    if (n_logits > 0) {
+        // Head (src/model.rs:190-216): final RMSNorm of the last n rows, the tied table in
+        // chunks (one chunk when resident), then the per-row argmax on the device.
+        const int n = int(n_logits);
+        rms_norm(x + size_t(T - n) * h, fnorm_.as<float>(), h, c.eps, n, hf_.as<float>(), s);
+        float* logits = logits_.as<float>();
+        const int S = prov_->head_splits;
+        for (size_t ci = 0; ci < prov_->n_head_chunks(); ci++) {
+            HeadChunk hc = prov_->head_chunk(ci);
+            const int rows_pad = hc.mat.n_strips * STRIP;
+            if (S == 1 && hc.first == 0 && size_t(rows_pad) == vpad_) {
+                matvec(hc.mat, hf_.as<float>(), h, n, logits, 1, s);
+            } else {
+                matvec(hc.mat, hf_.as<float>(), h, n, part, S, s);
+                reduce_store(part, S, n, int(hc.rows), rows_pad, nullptr, logits + hc.first, int(vpad_), s);
+            }
+            prov_->release_head_chunk(ci);
+        }
+        argmax_rows(logits, int(vpad_), int(c.vocab), n, pval_.as<float>(), pidx_.as<int>(), amax_.as<uint32_t>(), s);
+    }
+    prov_->end_forward();
+    pos_ += t;
+}
+
+void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax) {
+    HIPC(hipSetDevice(device_));
+    check_request(tok, n);
+    const size_t n_chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
+    for (size_t ci = 0; ci < n_chunks; ci++) {
+        const size_t a = ci * PREFILL_CHUNK, len = std::min(PREFILL_CHUNK, n - a);
+        forward_chunk(tok + a, len, ci + 1 == n_chunks ? 1 : 0);
+    }
+    if (logits) HIPC(hipMemcpyAsync(logits, logits_.p, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
+    if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    if (argmax) *argmax = h_out_.as<uint32_t>()[0];
+}
+
+void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float* logits, uint32_t* argmax) {
+    HIPC(hipSetDevice(device_));
+    check_request(tok, n);
+    if (n_logits == 0 || n_logits > n)
+        fail("asked for logits at " + std::to_string(n_logits) + " positions of " + std::to_string(n) + " tokens");
+    if (n > PREFILL_CHUNK) fail("forward_multi takes at most 128 tokens at a time");
+    forward_chunk(tok, n, n_logits);
+    if (logits)
+        HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.p, vpad_ * 4, cfg_.vocab * 4, n_logits, hipMemcpyDeviceToHost,
+                              stream_));
+    if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, n_logits * 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    if (argmax) std::memcpy(argmax, h_out_.p, n_logits * 4);
+}
+
+void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t* next) {
+    HIPC(hipSetDevice(device_));
+    check_request(block, n);
+    if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
+    const size_t p = pos_;
+    HIPC(hipEventRecord(ev0_, stream_));
+    forward_chunk(block, n, n);
+    accept_greedy(amax_.as<uint32_t>(), tok_.as<uint32_t>(), int(n), acc_.as<uint32_t>(), stream_);
+    HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipEventRecord(ev1_, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    float ms = 0;
+    HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    last_step_ms_ = ms;
+    const uint32_t* o = h_out_.as<uint32_t>();
+    *m = o[0];
+    *next = o[1];
+    pos_ = p + o[0] + 1;  // truncate(p + m + 1), src/spec.rs:137-139
+}
+
+}  // namespace ls

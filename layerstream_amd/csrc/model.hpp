@@ -1,0 +1,128 @@
+// The device-side Model (src/model.rs:16-140) and its weight providers (src/provider.rs).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "source.hpp"
+
+namespace ls {
+
+void hip_check(hipError_t e, const char* what);
+#define HIPC(x) ::ls::hip_check((x), #x)
+
+// Device allocation owned by one object.
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t bytes);
+    ~DevBuf();
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// Pinned host allocation (hipHostMalloc).
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    PinnedBuf() = default;
+    explicit PinnedBuf(size_t bytes);
+    ~PinnedBuf();
+    PinnedBuf(const PinnedBuf&) = delete;
+    PinnedBuf& operator=(const PinnedBuf&) = delete;
+    PinnedBuf(PinnedBuf&& o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+    PinnedBuf& operator=(PinnedBuf&& o) noexcept;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// One transformer layer on the device: q/k/v fused into one matrix (rows h, kv, kv), gate and
+// up fused (rows inter, inter), plus f32 bias and norm vectors.
+struct DevLayer {
+    DevMat qkv, o, gu, down;
+    const float* b_qkv = nullptr;
+    const float* in_norm = nullptr;
+    const float* post_norm = nullptr;
+};
+
+// Byte offsets of one layer (or one head chunk) inside a device arena.
+struct LayerArena {
+    size_t qkv_d, qkv_s, o_d, o_s, gu_d, gu_s, down_d, down_s, b_qkv, in_norm, post_norm, total;
+};
+LayerArena layer_arena(const Config& c);
+DevLayer bind_layer(const Config& c, const LayerArena& a, uint8_t* base);
+DevMat bind_mat(uint8_t* data, uint16_t* scales, const Format& f, int rows, int cols);
+// Convert a raw layer block (reference layout, already on the device) into the arena.
+void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* raw_dev, const LayerArena& a, uint8_t* base,
+                        hipStream_t s);
+
+struct HeadChunk {
+    size_t first = 0, rows = 0;
+    DevMat mat;
+};
+
+constexpr size_t HEAD_ROWS = 4096;  // src/provider.rs:21
+
+class DeviceProvider {
+public:
+    virtual ~DeviceProvider() = default;
+    virtual const char* name() const = 0;
+    virtual void begin_forward(bool with_head) = 0;
+    virtual const DevLayer& layer(size_t l) = 0;  // ordered before later work on the compute stream
+    virtual void release_layer(size_t l) = 0;     // the compute stream has every kernel of layer l
+    virtual size_t n_head_chunks() const = 0;
+    virtual HeadChunk head_chunk(size_t c) = 0;
+    virtual void release_head_chunk(size_t c) = 0;
+    virtual void end_forward() = 0;
+    // x[t][h] = embedding rows of host tokens (device tokens copy for the resident table).
+    virtual void embed(const uint32_t* host_tokens, const uint32_t* dev_tokens, int t, float* x) = 0;
+    virtual ls_report report() const = 0;
+    int head_splits = 1;  // K split of the output head, the same in every mode
+};
+
+std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t compute);
+std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStream_t compute);
+
+class Model {
+public:
+    Model(const Source& src, int mode, int slots, size_t max_ctx, int device);
+    ~Model();
+    const Config& cfg() const { return cfg_; }
+    size_t pos() const { return pos_; }
+    size_t max_ctx() const { return max_ctx_; }
+    void reset() { pos_ = 0; }
+    void truncate(size_t pos);
+    // Model::forward: logits/argmax of the last token (each may be null).
+    void forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax);
+    void forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float* logits, uint32_t* argmax);
+    void verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t* next);
+    ls_report report() const { return prov_->report(); }
+    double last_step_ms() const { return last_step_ms_; }
+    int device() const { return device_; }
+
+private:
+    void check_request(const uint32_t* tok, size_t n) const;
+    void forward_chunk(const uint32_t* tok, size_t t, size_t n_logits);
+
+    Config cfg_;
+    int device_;
+    size_t max_ctx_, pos_ = 0;
+    hipStream_t stream_ = nullptr;
+    std::unique_ptr<DeviceProvider> prov_;
+    DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_;
+    DevBuf x_, xn_, qkv_, attn_, gu_, act_, part_, scores_, logits_, hf_, amax_, pval_, pidx_, tok_, acc_;
+    PinnedBuf h_tok_, h_out_;
+    size_t part_floats_ = 0, vpad_ = 0;
+    int s_qkv_ = 1, s_o_ = 1, s_gu_ = 1, s_down_ = 1;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+    double last_step_ms_ = 0;
+};
+
+}  // namespace ls

@@ -1,0 +1,315 @@
+"""Parity of the HIP engine (through the C ABI) with the oracle, on an MI355X.
+
+Tolerances: logits within 1e-4 * (1 + max|ref|) on the tiny models and 1e-3 relative on the
+0.5B shape (the north star's bound); token sequences, accepted counts and argmax exactly.
+Within the GPU engine, batched and single-token passes, and resident and streamed weights, are
+compared bit for bit.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import layerstream_amd as LS
+import oracle_py as O
+import tinymodels as T
+
+pytestmark = pytest.mark.gpu
+
+PROMPT = [5, 17, 301, 42, 599, 0]
+OTHER_PROMPT = [250, 3, 77]
+FOLLOW = [7, 33, 120]
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_cfg(text):
+    c = LS.config_from_json(text)
+    return {k: c[k] for k in ("format", "embed_format", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "vocab", "eps", "rope_theta")}
+
+
+def gpu_model(m, mode=LS.MODE_RESIDENT, slots=2, max_ctx=128):
+    src = LS.Source.from_memory(m["config_text"], m["layers"], m["embed"], m["norm"])
+    return LS.Model(src, mode, slots, max_ctx)
+
+
+def cpu_model(m, max_ctx=128):
+    return O.OracleModel(oracle_cfg(m["config_text"]), m["layers"], m["embed"], m["norm"], threads=os.cpu_count() or 4, max_ctx=max_ctx)
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def close(got, ref, rel=1e-4):
+    got, ref = np.asarray(got), np.asarray(ref)
+    return np.max(np.abs(got - ref)) <= rel * (1 + np.max(np.abs(ref)))
+
+
+# ------------------------------------------------------------------------------ operator
+@pytest.mark.parametrize("f", [(16, 0), (8, 32), (8, 64), (4, 16), (4, 32), (4, 64)])
+def test_matmul_matches_the_oracle_and_is_batch_invariant(f):
+    from hipmem import DeviceArray
+
+    say("matmul", f)
+    rng = np.random.default_rng(1)
+    pool = O.lib().or_pool_new(4)
+    try:
+        for rows, cols in [(37, 128), (64, 256), (150, 192)]:
+            if f[0] != 16 and cols % f[1]:
+                continue
+            w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+            if f[0] == 16:
+                wb = T.bf16_trunc_bytes(w.reshape(-1))
+            else:
+                wb = np.concatenate([LS.quantize_row(f, r)[0] for r in w])
+            dw = DeviceArray(wb)
+            for t in [1, 2, 5, 9, 16, 17, 33]:
+                x = rng.standard_normal((t, cols)).astype(np.float32)
+                ref = np.zeros(t * rows, np.float32)
+                O.lib().or_matmul(pool, O.fmt(*f), O.u8(wb), rows, cols, O.f32(x), t, O.f32(ref))
+                dx, dy = DeviceArray(x), DeviceArray(np.zeros(t * rows, np.float32))
+                LS._check(LS.lib().ls_matmul(LS.fmt(*f), dw.p, rows, cols, dx.p, t, dy.p, None))
+                y = dy.to_host(ref)
+                assert np.all(np.abs(y - ref) <= 1e-4 * (1 + np.abs(ref))), (f, rows, cols, t)
+                # each row of the batch equals the single-input product bit for bit
+                for tt in (0, t - 1):
+                    d1, o1 = DeviceArray(np.ascontiguousarray(x[tt])), DeviceArray(np.zeros(rows, np.float32))
+                    LS._check(LS.lib().ls_matmul(LS.fmt(*f), dw.p, rows, cols, d1.p, 1, o1.p, None))
+                    y1 = o1.to_host(np.zeros(rows, np.float32))
+                    assert np.array_equal(bits(y1), bits(y[tt * rows : (tt + 1) * rows])), (f, t, tt)
+    finally:
+        O.lib().or_pool_free(pool)
+
+
+# ------------------------------------------------------------------------------ tiny models
+MODELS = {}
+
+
+def tiny(name):
+    if name not in MODELS:
+        base = T.write_tiny_model(13)
+        if name == "bf16":
+            MODELS[name] = base
+        elif name == "int8":
+            MODELS[name] = T.quantized(base, (8, 32), (8, 32))
+        elif name == "int4":
+            MODELS[name] = T.quantized(base, (4, 32), (4, 32))
+        elif name == "mixed":
+            MODELS[name] = T.quantized(base, (4, 16), (8, 64))
+        elif name == "unrelated":
+            MODELS[name] = T.write_tiny_model(99)
+    return MODELS[name]
+
+
+def run_fixed(m):
+    out = [m.forward(PROMPT)]
+    for t in FOLLOW:
+        out.append(m.forward([t]))
+    return np.stack(out)
+
+
+def run_greedy(m):
+    out = [m.forward(PROMPT)]
+    for _ in range(3):
+        out.append(m.forward([int(np.argmax(out[-1]))]))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("name", ["bf16", "int8", "int4", "mixed"])
+def test_tiny_model_logits_match_the_oracle(name):
+    say("tiny logits", name)
+    m = tiny(name)
+    ref = run_fixed(cpu_model(m))
+    for mode in (LS.MODE_RESIDENT, LS.MODE_STREAM):
+        got = run_fixed(gpu_model(m, mode))
+        assert close(got, ref), (name, mode, np.max(np.abs(got - ref)))
+        assert np.array_equal(got.argmax(1), ref.argmax(1))
+
+
+def test_checking_several_positions_at_once_gives_bit_identical_logits():
+    """tests/spec.rs:63-84 on the device, for every format and both modes."""
+    block = [8, 9, 400, 33, 120]
+    for name in ("bf16", "int8", "int4"):
+        for mode in (LS.MODE_RESIDENT, LS.MODE_STREAM):
+            say("batch invariance", name, mode)
+            m = tiny(name)
+            for n in (1, 2, len(block)):
+                a = gpu_model(m, mode)
+                a.forward(PROMPT)
+                together = a.forward_multi(block, n)
+                b = gpu_model(m, mode)
+                b.forward(PROMPT)
+                one = np.stack([b.forward([t]) for t in block])
+                assert np.array_equal(bits(together), bits(one[len(block) - n :])), (name, mode, n)
+                assert a.pos() == b.pos()
+
+
+def test_every_mode_gives_bit_identical_logits():
+    """tests/pipeline.rs:79-101 and tests/quant.rs:142-158: resident vs 1, 2, 3 slots."""
+    for name in ("bf16", "mixed"):
+        m = tiny(name)
+        ref = run_greedy(gpu_model(m, LS.MODE_RESIDENT))
+        for slots in (1, 2, 3):
+            say("modes", name, slots)
+            got = run_greedy(gpu_model(m, LS.MODE_STREAM, slots))
+            assert np.array_equal(bits(ref), bits(got)), (name, slots)
+
+
+def test_streaming_reads_every_layer_and_the_table_once_per_pass():
+    """tests/quant.rs:232-248: 4 passes x (layers + table) + one row per input token."""
+    m = tiny("int4")
+    src = LS.Source.from_lsq_image(np.frombuffer(m["lsq"], np.uint8).copy())
+    g = LS.Model(src, LS.MODE_STREAM, 2, 64)
+    run_greedy(g)
+    c = src.config()
+    _, total = LS.layer_layout(m["config_text"])
+    rb = LS.row_bytes(c["embed_format"], c["hidden"])
+    per_pass = c["layers"] * total + c["vocab"] * rb
+    assert src.bytes_read() == 4 * per_pass + 9 * rb
+    rep = g.report()
+    assert rep["resident_weight_bytes"] > 0
+
+
+def test_truncate_incremental_and_bad_requests():
+    m = tiny("bf16")
+    a = gpu_model(m)
+    a.forward(PROMPT)
+    a.forward([7, 8, 9])
+    a.truncate(len(PROMPT))
+    after = a.forward([20])
+    b = gpu_model(m)
+    b.forward(PROMPT)
+    assert np.array_equal(bits(after), bits(b.forward([20])))
+    with pytest.raises(LS.LayerstreamError):
+        a.truncate(a.pos() + 1)
+    # incremental == whole prompt (tests/pipeline.rs:200-217)
+    toks = [(i * 31 + 7) % T.VOCAB for i in range(20)]
+    whole = gpu_model(m, max_ctx=64).forward(toks)
+    inc = gpu_model(m, max_ctx=64)
+    inc.forward(toks[:9])
+    for t in toks[9:19]:
+        inc.forward([t])
+    got = inc.forward(toks[19:])
+    assert np.max(np.abs(whole - got)) < 1e-4 and inc.pos() == 20
+    # bad requests are errors (tests/pipeline.rs:219-232)
+    o = gpu_model(m, max_ctx=64)
+    for bad in ([], [T.VOCAB], [1] * 65):
+        with pytest.raises(LS.LayerstreamError):
+            o.forward(bad)
+    o.forward([1] * 60)
+    with pytest.raises(LS.LayerstreamError):
+        o.forward([1] * 5)
+    o.reset()
+    o.forward([1] * 64)
+    t = gpu_model(m)
+    for toks, n in ([1, 2], 3), ([1, 2], 0):
+        with pytest.raises(LS.LayerstreamError):
+            t.forward_multi(toks, n)
+
+
+def test_speculation_never_changes_the_output_and_matches_the_oracle():
+    """tests/spec.rs:103-132 with draft models on the device, plus token parity with the oracle."""
+    base = tiny("bf16")
+    for dname in ("int8", "int4", "unrelated"):
+        for prompt in (PROMPT, OTHER_PROMPT):
+            for max_new in (1, 2, 9, 30):
+                want = O.plain_greedy(cpu_model(base), prompt, max_new)
+                assert LS.greedy_generate(gpu_model(base), prompt, max_new) == want
+                for k in (1, 2, 3, 5, 8):
+                    for mode in (LS.MODE_RESIDENT, LS.MODE_STREAM):
+                        got, st = LS.speculative_greedy(gpu_model(base, mode), gpu_model(tiny(dname)), prompt, max_new, k)
+                        assert got == want, (dname, len(prompt), max_new, k, mode)
+                        assert st["accepted"] <= st["drafted"]
+                        assert st["target_passes"] <= max(len(got) - 1, 0)
+        say("spec", dname, "ok")
+
+
+def test_eos_and_perfect_draft():
+    m = tiny("bf16")
+    full = O.plain_greedy(cpu_model(m), PROMPT, 24)
+    for cut in (0, 1, 5, 11):
+        eos = [full[cut]]
+        want = O.plain_greedy(cpu_model(m), PROMPT, 24, eos)
+        for k in (1, 4, 8):
+            got, _ = LS.speculative_greedy(gpu_model(m), gpu_model(m), PROMPT, 24, k, eos)
+            assert got == want, (cut, k)
+    max_new, k = 21, 3
+    want = O.plain_greedy(cpu_model(m), PROMPT, max_new)
+    got, st = LS.speculative_greedy(gpu_model(m), gpu_model(m), PROMPT, max_new, k)
+    assert got == want and st["accepted"] == st["drafted"]
+    assert st["target_passes"] == -(-(max_new - 1) // (k + 1))
+    # bad requests (tests/spec.rs:175-193)
+    for kk, prompt, mn in [(0, PROMPT, 5), (33, PROMPT, 5), (2, [], 5), (2, PROMPT, 0), (2, PROMPT, 500)]:
+        with pytest.raises(LS.LayerstreamError):
+            LS.speculative_greedy(gpu_model(m), gpu_model(m), prompt, mn, kk)
+    t = gpu_model(m)
+    t.forward(PROMPT)
+    with pytest.raises(LS.LayerstreamError):
+        LS.speculative_greedy(t, gpu_model(m), PROMPT, 5, 2)
+
+
+def test_verify_step_accepts_the_longest_matching_prefix():
+    m = tiny("bf16")
+    g = O.plain_greedy(cpu_model(m), PROMPT, 12)
+    for m_want in range(0, 6):
+        tgt = gpu_model(m)
+        a = tgt.forward_argmax(PROMPT)
+        assert a == g[0]
+        drafts = list(g[1 : 1 + m_want]) + [(g[1 + m_want] + 1) % T.VOCAB] + [3] * (5 - m_want)
+        drafts = drafts[:5]
+        acc, nxt = tgt.verify_greedy([a] + drafts)
+        want_m = min(m_want, 5)
+        assert acc == want_m and nxt == g[1 + want_m], (m_want, acc, nxt)
+        assert tgt.pos() == len(PROMPT) + acc + 1
+
+
+# ------------------------------------------------------------------------------ 0.5B shape
+def qwen05b(fmt=None, seed=1):
+    text = LS.qwen2_config_text(**LS.QWEN2_05B)
+    m = LS.synth_bf16_model(text, seed)
+    if fmt is None:
+        return m
+    img = LS.quantize_model(text, m["layers"], m["embed"], m["norm"], fmt)
+    parts = T.split_lsq(img.tobytes(), oracle_cfg(LS.inject_quant(text, *fmt)))
+    return {"config_text": LS.inject_quant(text, *fmt), "lsq": img, **{k: parts[k] for k in ("layers", "embed", "norm")}}
+
+
+def test_qwen05b_bf16_verify_step_matches_the_oracle():
+    """The CPU-runnable configuration: 0.5B shape, bf16 weights, f32 compute, prompt of 64 random
+    ids, one verify step of k=4 drafts whose first two are the greedy continuation."""
+    say("0.5B bf16: synth")
+    m = qwen05b()
+    rng = np.random.default_rng(64)
+    prompt = rng.integers(0, 151936, 64).tolist()
+    cpu = cpu_model(m, max_ctx=256)
+    g = O.plain_greedy(cpu, prompt, 3)  # a, g1, g2
+    cpu.reset()
+    drafts = [g[1], g[2]] + rng.integers(0, 151936, 2).tolist()
+    block = [g[0]] + drafts
+    say("0.5B bf16: oracle")
+    cpu.forward(prompt)
+    ref = cpu.forward_multi(block, 5)
+    say("0.5B bf16: gpu")
+    gm = gpu_model(m, max_ctx=256)
+    a = gm.forward_argmax(prompt)
+    assert a == g[0]
+    got = gm.forward_multi(block, 5)
+    rel = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    say("max rel logit diff", rel)
+    assert rel <= 1e-3
+    assert np.array_equal(got.argmax(1), ref.argmax(1))
+    top2 = np.sort(ref, axis=1)[:, -2:]
+    say("top1-top2 margins", (top2[:, 1] - top2[:, 0]).tolist())
+    # the fused verify step gives the same acceptance
+    gm2 = gpu_model(m, max_ctx=256)
+    gm2.forward(prompt)
+    acc, nxt = gm2.verify_greedy(block)
+    want_m = 0
+    while want_m < 4 and ref[want_m].argmax() == drafts[want_m]:
+        want_m += 1
+    assert acc == want_m >= 2 and nxt == ref[want_m].argmax()
