@@ -159,6 +159,19 @@ int ls_model_report(const ls_model* m, ls_report* out);
 /* Time of the last verify step on the device (HIP events around its kernels), in ms. */
 double ls_model_last_step_ms(const ls_model* m);
 
+/* Profiling of the weight-streaming matvec kernels: with enable != 0, HIP events bracket each
+ * launch on the model's compute stream; ls_model_profile_read returns the launches, their summed
+ * device time and their algorithmic bytes (weights in the stored format + f32 inputs + f32
+ * outputs) since the last read, then resets. */
+typedef struct {
+    uint64_t launches;
+    double ms;
+    double bytes;
+    double flops;
+} ls_kernel_stat;
+int ls_model_profile(ls_model* m, int enable);
+int ls_model_profile_read(ls_model* m, ls_kernel_stat* out);
+
 /* ---------------------------------------------------------------------------------------
  * Speculative decoding: speculative_greedy (src/spec.rs:57-152).
  * ------------------------------------------------------------------------------------- */
@@ -198,6 +211,19 @@ void ls_drafter_free(ls_drafter* d);
 int ls_speculative_greedy(ls_model* target, ls_drafter* draft, const uint32_t* prompt, size_t n_prompt,
                           size_t max_new, size_t k, const uint32_t* eos, size_t n_eos, uint32_t* out,
                           size_t* out_len, ls_spec_stats* stats);
+/* The same loop in resumable form: begin runs the prompt pass (src/spec.rs:82-92), step runs
+ * up to max_steps verify passes (0 = until generation ends; *done = 1 then), result copies the
+ * tokens so far. Used by benchmarks to time exactly K verify passes. */
+typedef struct ls_spec ls_spec;
+int ls_spec_begin(ls_model* target, ls_drafter* draft, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                  size_t k, const uint32_t* eos, size_t n_eos, ls_spec** out);
+int ls_spec_step(ls_spec* s, size_t max_steps, int* done);
+int ls_spec_result(const ls_spec* s, uint32_t* out, size_t cap, size_t* out_len, ls_spec_stats* stats);
+/* Device time (ms, HIP events around each fused verify) and accepted count m of every verify
+ * pass so far. Returns the number of passes; copies at most cap entries (arrays may be NULL). */
+size_t ls_spec_step_log(const ls_spec* s, double* ms, uint32_t* accepted, size_t cap);
+void ls_spec_free(ls_spec* s);
+
 /* Plain greedy decoding with Sampler::greedy (src/model.rs:328-336), the parity baseline of
  * tests/spec.rs:44-57. */
 int ls_greedy_generate(ls_model* m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const uint32_t* eos,

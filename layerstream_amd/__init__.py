@@ -86,6 +86,10 @@ class SpecStats(C.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
+class KernelStat(C.Structure):
+    _fields_ = [("launches", C.c_uint64), ("ms", C.c_double), ("bytes", C.c_double), ("flops", C.c_double)]
+
+
 PREFILL = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_uint32), C.c_size_t)
 PROPOSE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.c_size_t, C.POINTER(C.c_uint32))
 COMMIT = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_uint32), C.c_size_t, C.c_size_t)
@@ -132,6 +136,13 @@ SIGNATURES = {
     "ls_drafter_free": (None, [C.POINTER(Drafter)]),
     "ls_speculative_greedy": (C.c_int, [P, C.POINTER(Drafter), U32, SZ, SZ, SZ, U32, SZ, U32, C.POINTER(SZ), C.POINTER(SpecStats)]),
     "ls_greedy_generate": (C.c_int, [P, U32, SZ, SZ, U32, SZ, U32, C.POINTER(SZ)]),
+    "ls_spec_begin": (C.c_int, [P, C.POINTER(Drafter), U32, SZ, SZ, SZ, U32, SZ, C.POINTER(P)]),
+    "ls_spec_step": (C.c_int, [P, SZ, C.POINTER(C.c_int)]),
+    "ls_spec_result": (C.c_int, [P, U32, SZ, C.POINTER(SZ), C.POINTER(SpecStats)]),
+    "ls_spec_step_log": (SZ, [P, C.POINTER(C.c_double), U32, SZ]),
+    "ls_spec_free": (None, [P]),
+    "ls_model_profile": (C.c_int, [P, C.c_int]),
+    "ls_model_profile_read": (C.c_int, [P, C.POINTER(KernelStat)]),
     "ls_matmul": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
 }
 
@@ -390,6 +401,15 @@ class Model:
     def last_step_ms(self) -> float:
         return lib().ls_model_last_step_ms(self.h)
 
+    def profile(self, enable: bool):
+        """Bracket every weight-streaming matvec launch with HIP events (for roofline figures)."""
+        _check(lib().ls_model_profile(self.h, int(enable)))
+
+    def profile_read(self) -> dict:
+        st = KernelStat()
+        _check(lib().ls_model_profile_read(self.h, C.byref(st)))
+        return {f: getattr(st, f) for f, _ in KernelStat._fields_}
+
 
 class ModelDrafter:
     """A draft Model, as the reference's `draft: &mut Model` (src/spec.rs:59)."""
@@ -438,6 +458,56 @@ def speculative_greedy(target: Model, draft, prompt, max_new: int, k: int, eos=(
     rc = lib().ls_speculative_greedy(target.h, C.byref(draft.d), pp, p.size, max_new, k, _u32(e), len(eos), _u32(out), C.byref(n), C.byref(st))
     _check(rc)
     return out[: n.value].tolist(), st.as_dict()
+
+
+class SpecRun:
+    """speculative_greedy in resumable form: the prompt pass at construction, then step(n) runs n
+    verify passes; tokens(), stats() and step_log() report progress."""
+
+    def __init__(self, target: Model, draft, prompt, max_new: int, k: int, eos=()):
+        if isinstance(draft, Model):
+            draft = ModelDrafter(draft)
+        self._draft = draft
+        p = _toks(prompt)
+        e = _toks(list(eos) or [0])
+        h = C.c_void_p()
+        _check(lib().ls_spec_begin(target.h, C.byref(draft.d), _u32(p), p.size, max_new, k, _u32(e), len(eos), C.byref(h)))
+        self.h = h
+        self.max_new = max_new
+
+    def step(self, n: int = 1) -> bool:
+        done = C.c_int(0)
+        _check(lib().ls_spec_step(self.h, n, C.byref(done)))
+        return bool(done.value)
+
+    def tokens(self):
+        out = np.zeros(max(self.max_new, 1), np.uint32)
+        n = C.c_size_t(0)
+        _check(lib().ls_spec_result(self.h, _u32(out), out.size, C.byref(n), None))
+        return out[: n.value].tolist()
+
+    def stats(self) -> dict:
+        st = SpecStats()
+        _check(lib().ls_spec_result(self.h, None, 0, None, C.byref(st)))
+        return st.as_dict()
+
+    def step_log(self):
+        n = lib().ls_spec_step_log(self.h, None, None, 0)
+        ms = np.zeros(max(n, 1), np.float64)
+        m = np.zeros(max(n, 1), np.uint32)
+        lib().ls_spec_step_log(self.h, ms.ctypes.data_as(C.POINTER(C.c_double)), _u32(m), n)
+        return ms[:n], m[:n]
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ls_spec_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def greedy_generate(m: Model, prompt, max_new: int, eos=()):

@@ -15,6 +15,10 @@ struct ls_model {
     std::unique_ptr<ls::Model> m;
 };
 
+struct ls_spec {
+    std::unique_ptr<ls::SpecRun> r;
+};
+
 namespace {
 
 template <class F>
@@ -300,6 +304,64 @@ int ls_speculative_greedy(ls_model* target, ls_drafter* d, const uint32_t* promp
         std::memcpy(out, toks.data(), toks.size() * 4);
         *out_len = toks.size();
         if (stats) *stats = st;
+    });
+}
+
+int ls_spec_begin(ls_model* target, ls_drafter* d, const uint32_t* prompt, size_t n_prompt, size_t max_new, size_t k,
+                  const uint32_t* eos, size_t n_eos, ls_spec** out) {
+    return guard([&] {
+        need(target, "target");
+        need(d, "drafter");
+        need(out, "output");
+        auto s = std::make_unique<ls_spec>();
+        s->r = std::make_unique<ls::SpecRun>(*target->m, *d, prompt, n_prompt, max_new, k, eos, n_eos);
+        *out = s.release();
+    });
+}
+
+int ls_spec_step(ls_spec* s, size_t max_steps, int* done) {
+    return guard([&] {
+        need(s, "run");
+        for (size_t i = 0; (max_steps == 0 || i < max_steps) && !s->r->done(); i++) s->r->step();
+        if (done) *done = s->r->done() ? 1 : 0;
+    });
+}
+
+int ls_spec_result(const ls_spec* s, uint32_t* out, size_t cap, size_t* out_len, ls_spec_stats* stats) {
+    return guard([&] {
+        need(s, "run");
+        const auto& t = s->r->tokens();
+        if (out_len) *out_len = t.size();
+        if (out) std::memcpy(out, t.data(), std::min(cap, t.size()) * 4);
+        if (stats) *stats = s->r->stats();
+    });
+}
+
+size_t ls_spec_step_log(const ls_spec* s, double* ms, uint32_t* accepted, size_t cap) {
+    if (!s) return 0;
+    const auto& a = s->r->step_ms();
+    const auto& b = s->r->step_m();
+    for (size_t i = 0; i < std::min(cap, a.size()); i++) {
+        if (ms) ms[i] = a[i];
+        if (accepted) accepted[i] = b[i];
+    }
+    return a.size();
+}
+
+void ls_spec_free(ls_spec* s) { delete s; }
+
+int ls_model_profile(ls_model* m, int enable) {
+    return guard([&] {
+        need(m, "model");
+        m->m->set_profiling(enable != 0);
+    });
+}
+
+int ls_model_profile_read(ls_model* m, ls_kernel_stat* out) {
+    return guard([&] {
+        need(m, "model");
+        need(out, "output");
+        *out = m->m->read_profile();
     });
 }
 

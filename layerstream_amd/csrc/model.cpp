@@ -481,15 +481,16 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     amax_ = DevBuf(T * 4);
     pval_ = DevBuf(T * 64 * 4);
     pidx_ = DevBuf(T * 64 * 4);
-    tok_ = DevBuf(T * 4);
+    tok_ = DevBuf(max_ctx * 4);
     acc_ = DevBuf(16);
-    h_tok_ = PinnedBuf(T * 4);
+    h_tok_ = PinnedBuf(max_ctx * 4);
     h_out_ = PinnedBuf(T * 4 + 16);
     HIPC(hipStreamSynchronize(stream_));
 }
 
 Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    for (hipEvent_t e : prof_ev_) (void)hipEventDestroy(e);
     prov_.reset();
     if (ev0_) (void)hipEventDestroy(ev0_);
     if (ev1_) (void)hipEventDestroy(ev1_);
@@ -512,35 +513,78 @@ void Model::check_request(const uint32_t* tok, size_t n) const {
 }
 
 // forward_chunk (src/model.rs:161-220), all on the compute stream.
-void Model::forward_chunk(const uint32_t* tok, size_t t, size_t n_logits) {
+void Model::mv(const DevMat& W, const float* x, int ldx, int t, float* part, int splits) {
+    if (!prof_) {
+        matvec(W, x, ldx, t, part, splits, stream_);
+        return;
+    }
+    while (prof_ev_.size() < prof_used_ + 2) {
+        hipEvent_t e;
+        HIPC(hipEventCreate(&e));
+        prof_ev_.push_back(e);
+    }
+    HIPC(hipEventRecord(prof_ev_[prof_used_], stream_));
+    matvec(W, x, ldx, t, part, splits, stream_);
+    HIPC(hipEventRecord(prof_ev_[prof_used_ + 1], stream_));
+    prof_used_ += 2;
+    const Format f{W.bits, W.group};
+    prof_acc_.launches++;
+    prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * t * (double(W.cols) + double(W.rows));
+    prof_acc_.flops += 2.0 * t * double(W.rows) * double(W.cols);
+}
+
+// Sum the device time of the profiled launches (called after the stream has drained).
+void Model::harvest() {
+    for (size_t i = 0; i + 1 < prof_used_; i += 2) {
+        float ms = 0;
+        HIPC(hipEventElapsedTime(&ms, prof_ev_[i], prof_ev_[i + 1]));
+        prof_acc_.ms += ms;
+    }
+    prof_used_ = 0;
+}
+
+void Model::set_profiling(bool on) {
+    HIPC(hipStreamSynchronize(stream_));
+    harvest();
+    prof_ = on;
+    prof_acc_ = ls_kernel_stat{};
+}
+
+ls_kernel_stat Model::read_profile() {
+    HIPC(hipStreamSynchronize(stream_));
+    harvest();
+    ls_kernel_stat r = prof_acc_;
+    prof_acc_ = ls_kernel_stat{};
+    return r;
+}
+
+void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits) {
     const Config& c = cfg_;
     const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter), T = int(t);
     const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim), pos0 = int(pos_);
     hipStream_t s = stream_;
-    std::memcpy(h_tok_.p, tok, t * 4);
-    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, t * 4, hipMemcpyHostToDevice, s));
     float* x = x_.as<float>();
     float* xn = xn_.as<float>();
     float* qkv = qkv_.as<float>();
     float* part = part_.as<float>();
-    prov_->embed(tok, tok_.as<uint32_t>(), T, x);
+    prov_->embed(tok, dtok, T, x);
     prov_->begin_forward(n_logits > 0);
     for (size_t l = 0; l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
         float* kc = kcache_.as<float>() + l * max_ctx_ * kv;
         float* vc = vcache_.as<float>() + l * max_ctx_ * kv;
         rms_norm(x, L.in_norm, h, c.eps, T, xn, s);
-        matvec(L.qkv, xn, h, T, part, s_qkv_, s);
+        mv(L.qkv, xn, h, T, part, s_qkv_);
         reduce_store(part, s_qkv_, T, h + 2 * kv, L.qkv.n_strips * STRIP, L.b_qkv, qkv, h + 2 * kv, s);
         rope_append_kv(qkv, T, heads, kvh, hd, pos0, rope_cos_.as<float>(), rope_sin_.as<float>(), kc, vc, s);
         attention(qkv, T, heads, kvh, hd, pos0, int(max_ctx_), kc, vc, scores_.as<float>(), attn_.as<float>(), s);
-        matvec(L.o, attn_.as<float>(), h, T, part, s_o_, s);
+        mv(L.o, attn_.as<float>(), h, T, part, s_o_);
         reduce_residual(part, s_o_, T, h, L.o.n_strips * STRIP, x, h, s);
         rms_norm(x, L.post_norm, h, c.eps, T, xn, s);
-        matvec(L.gu, xn, h, T, part, s_gu_, s);
+        mv(L.gu, xn, h, T, part, s_gu_);
         reduce_store(part, s_gu_, T, 2 * in, L.gu.n_strips * STRIP, nullptr, gu_.as<float>(), 2 * in, s);
         silu_mul(gu_.as<float>(), T, in, act_.as<float>(), s);
-        matvec(L.down, act_.as<float>(), in, T, part, s_down_, s);
+        mv(L.down, act_.as<float>(), in, T, part, s_down_);
         reduce_residual(part, s_down_, T, h, L.down.n_strips * STRIP, x, h, s);
         prov_->release_layer(l);
     }
@@ -555,9 +599,9 @@ void Model::forward_chunk(const uint32_t* tok, size_t t, size_t n_logits) {
             HeadChunk hc = prov_->head_chunk(ci);
             const int rows_pad = hc.mat.n_strips * STRIP;
             if (S == 1 && hc.first == 0 && size_t(rows_pad) == vpad_) {
-                matvec(hc.mat, hf_.as<float>(), h, n, logits, 1, s);
+                mv(hc.mat, hf_.as<float>(), h, n, logits, 1);
             } else {
-                matvec(hc.mat, hf_.as<float>(), h, n, part, S, s);
+                mv(hc.mat, hf_.as<float>(), h, n, part, S);
                 reduce_store(part, S, n, int(hc.rows), rows_pad, nullptr, logits + hc.first, int(vpad_), s);
             }
             prov_->release_head_chunk(ci);
@@ -568,17 +612,27 @@ void Model::forward_chunk(const uint32_t* tok, size_t t, size_t n_logits) {
     pos_ += t;
 }
 
+// Copy a call's tokens to the device once. The pinned staging buffer holds max_ctx tokens and
+// is only rewritten by the next call, after this call has drained the stream.
+const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
+    std::memcpy(h_tok_.p, tok, n * 4);
+    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
+    return tok_.as<uint32_t>();
+}
+
 void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax) {
     HIPC(hipSetDevice(device_));
     check_request(tok, n);
+    const uint32_t* dtok = stage_tokens(tok, n);
     const size_t n_chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
     for (size_t ci = 0; ci < n_chunks; ci++) {
         const size_t a = ci * PREFILL_CHUNK, len = std::min(PREFILL_CHUNK, n - a);
-        forward_chunk(tok + a, len, ci + 1 == n_chunks ? 1 : 0);
+        forward_chunk(tok + a, dtok + a, len, ci + 1 == n_chunks ? 1 : 0);
     }
     if (logits) HIPC(hipMemcpyAsync(logits, logits_.p, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
     if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
+    harvest();
     if (argmax) *argmax = h_out_.as<uint32_t>()[0];
 }
 
@@ -588,12 +642,13 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
     if (n_logits == 0 || n_logits > n)
         fail("asked for logits at " + std::to_string(n_logits) + " positions of " + std::to_string(n) + " tokens");
     if (n > PREFILL_CHUNK) fail("forward_multi takes at most 128 tokens at a time");
-    forward_chunk(tok, n, n_logits);
+    forward_chunk(tok, stage_tokens(tok, n), n, n_logits);
     if (logits)
         HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.p, vpad_ * 4, cfg_.vocab * 4, n_logits, hipMemcpyDeviceToHost,
                               stream_));
     if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, n_logits * 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
+    harvest();
     if (argmax) std::memcpy(argmax, h_out_.p, n_logits * 4);
 }
 
@@ -603,11 +658,13 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
     const size_t p = pos_;
     HIPC(hipEventRecord(ev0_, stream_));
-    forward_chunk(block, n, n);
-    accept_greedy(amax_.as<uint32_t>(), tok_.as<uint32_t>(), int(n), acc_.as<uint32_t>(), stream_);
+    const uint32_t* dtok = stage_tokens(block, n);
+    forward_chunk(block, dtok, n, n);
+    accept_greedy(amax_.as<uint32_t>(), dtok, int(n), acc_.as<uint32_t>(), stream_);
     HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
     HIPC(hipEventRecord(ev1_, stream_));
     HIPC(hipStreamSynchronize(stream_));
+    harvest();
     float ms = 0;
     HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
     last_step_ms_ = ms;

@@ -106,10 +106,16 @@ public:
     ls_report report() const { return prov_->report(); }
     double last_step_ms() const { return last_step_ms_; }
     int device() const { return device_; }
+    void set_profiling(bool on);
+    ls_kernel_stat read_profile();
 
 private:
     void check_request(const uint32_t* tok, size_t n) const;
-    void forward_chunk(const uint32_t* tok, size_t t, size_t n_logits);
+    void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits);
+    const uint32_t* stage_tokens(const uint32_t* tok, size_t n);
+    // A weight-streaming matvec, bracketed by profiling events when enabled.
+    void mv(const DevMat& W, const float* x, int ldx, int t, float* part, int splits);
+    void harvest();
 
     Config cfg_;
     int device_;
@@ -123,6 +129,10 @@ private:
     int s_qkv_ = 1, s_o_ = 1, s_gu_ = 1, s_down_ = 1;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
+    bool prof_ = false;
+    std::vector<hipEvent_t> prof_ev_;
+    size_t prof_used_ = 0;
+    ls_kernel_stat prof_acc_{};
 };
 
 }  // namespace ls

@@ -115,9 +115,9 @@ static void check_cb(int rc, const char* what) {
     if (rc < 0) fail(std::string("drafter ") + what + " failed");
 }
 
-std::vector<uint32_t> speculative_greedy(Model& target, ls_drafter& d, const uint32_t* prompt, size_t n_prompt, size_t max_new,
-                                         size_t k, const uint32_t* eos, size_t n_eos, ls_spec_stats& st) {
-    st = ls_spec_stats{};
+SpecRun::SpecRun(Model& target, ls_drafter& d, const uint32_t* prompt, size_t n_prompt, size_t max_new, size_t k,
+                 const uint32_t* eos, size_t n_eos)
+    : target_(target), d_(d), max_new_(max_new), k_(k), eos_(eos, eos + n_eos) {
     if (k == 0 || k > MAX_DRAFT) fail("k must be between 1 and 32, not " + std::to_string(k));
     if (n_prompt == 0 || max_new == 0 || !prompt) fail("need a prompt and at least one token to generate");
     Model* dm = is_model_drafter(d) ? static_cast<Model*>(d.ctx) : nullptr;
@@ -129,51 +129,59 @@ std::vector<uint32_t> speculative_greedy(Model& target, ls_drafter& d, const uin
     if (!d.prefill || !d.propose || !d.commit) fail("incomplete drafter");
 
     const double t0 = now_s();
-    uint32_t a;
-    target.forward(prompt, n_prompt, nullptr, &a);
+    target.forward(prompt, n_prompt, nullptr, &a_);
     check_cb(d.prefill(d.ctx, prompt, n_prompt), "prefill");
-    st.first_secs = now_s() - t0;
+    st_.first_secs = now_s() - t0;
+    out_.reserve(max_new);
+    out_.push_back(a_);
+    stop_ = contains(eos_.data(), eos_.size(), a_);
+    t_dec_ = now_s();
+}
 
-    std::vector<uint32_t> out;
-    out.reserve(max_new);
-    out.push_back(a);
-    bool stop = contains(eos, n_eos, a);
-    const double t_dec = now_s();
+void SpecRun::step() {
+    if (done()) return;
+    const size_t kk = std::min(k_, max_new_ - out_.size() - 1);  // a pass yields at most kk + 1 tokens
     uint32_t block[MAX_DRAFT + 1];
-    while (!stop && out.size() < max_new) {
-        const size_t kk = std::min(k, max_new - out.size() - 1);
-        double ts = now_s();
-        block[0] = a;
-        int f = d.propose(d.ctx, a, kk, block + 1);
-        check_cb(f, "propose");
-        st.draft_forwards += uint64_t(f);
-        st.draft_secs += now_s() - ts;
+    double ts = now_s();
+    block[0] = a_;
+    int f = d_.propose(d_.ctx, a_, kk, block + 1);
+    check_cb(f, "propose");
+    st_.draft_forwards += uint64_t(f);
+    st_.draft_secs += now_s() - ts;
 
-        const size_t p = target.pos();
-        ts = now_s();
-        uint32_t m, next;
-        target.verify_greedy(block, kk + 1, &m, &next);  // one weight pass checks every guess
-        st.target_secs += now_s() - ts;
-        st.target_passes++;
-        st.drafted += kk;
-        st.accepted += m;
-        for (size_t i = 0; i <= m; i++) {
-            const uint32_t tok = i < m ? block[i + 1] : next;
-            out.push_back(tok);
-            if (contains(eos, n_eos, tok) || out.size() == max_new) {
-                stop = true;
-                break;
-            }
+    const size_t p = target_.pos();
+    ts = now_s();
+    uint32_t m, next;
+    target_.verify_greedy(block, kk + 1, &m, &next);  // one weight pass checks every guess
+    st_.target_secs += now_s() - ts;
+    st_.target_passes++;
+    st_.drafted += kk;
+    st_.accepted += m;
+    step_ms_.push_back(target_.last_step_ms());
+    step_m_.push_back(m);
+    for (size_t i = 0; i <= m; i++) {
+        const uint32_t tok = i < m ? block[i + 1] : next;
+        out_.push_back(tok);
+        if (contains(eos_.data(), eos_.size(), tok) || out_.size() == max_new_) {
+            stop_ = true;
+            break;
         }
-        ts = now_s();
-        f = d.commit(d.ctx, block, p, m);
-        check_cb(f, "commit");
-        st.draft_forwards += uint64_t(f);
-        st.draft_secs += now_s() - ts;
-        a = next;
     }
-    st.decode_secs = now_s() - t_dec;
-    return out;
+    ts = now_s();
+    f = d_.commit(d_.ctx, block, p, m);
+    check_cb(f, "commit");
+    st_.draft_forwards += uint64_t(f);
+    st_.draft_secs += now_s() - ts;
+    a_ = next;
+    st_.decode_secs = now_s() - t_dec_;
+}
+
+std::vector<uint32_t> speculative_greedy(Model& target, ls_drafter& d, const uint32_t* prompt, size_t n_prompt, size_t max_new,
+                                         size_t k, const uint32_t* eos, size_t n_eos, ls_spec_stats& st) {
+    SpecRun run(target, d, prompt, n_prompt, max_new, k, eos, n_eos);
+    while (!run.done()) run.step();
+    st = run.stats();
+    return run.tokens();
 }
 
 std::vector<uint32_t> greedy_generate(Model& m, const uint32_t* prompt, size_t n_prompt, size_t max_new, const uint32_t* eos,

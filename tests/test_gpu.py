@@ -212,6 +212,26 @@ def test_truncate_incremental_and_bad_requests():
             t.forward_multi(toks, n)
 
 
+def test_prompts_longer_than_one_prefill_chunk():
+    """Prompts span several 128-token chunks (src/model.rs:111-119); each chunk must see its own
+    tokens and the cache of the chunks before it."""
+    rng = np.random.default_rng(7)
+    for name in ("bf16", "int4"):
+        m = tiny(name)
+        prompt = rng.integers(0, T.VOCAB, 300).tolist()
+        ref = cpu_model(m, max_ctx=512).forward(prompt)
+        for mode in (LS.MODE_RESIDENT, LS.MODE_STREAM):
+            say("long prompt", name, mode)
+            g = gpu_model(m, mode, max_ctx=512)
+            got = g.forward(prompt)
+            assert close(got, ref), (name, mode, np.max(np.abs(got - ref)))
+            inc = gpu_model(m, mode, max_ctx=512)
+            inc.forward(prompt[:150])
+            got2 = inc.forward(prompt[150:])
+            assert np.max(np.abs(got2 - got)) < 1e-4
+            assert g.pos() == inc.pos() == 300
+
+
 def test_speculation_never_changes_the_output_and_matches_the_oracle():
     """tests/spec.rs:103-132 with draft models on the device, plus token parity with the oracle."""
     base = tiny("bf16")
@@ -313,3 +333,33 @@ def test_qwen05b_bf16_verify_step_matches_the_oracle():
     while want_m < 4 and ref[want_m].argmax() == drafts[want_m]:
         want_m += 1
     assert acc == want_m >= 2 and nxt == ref[want_m].argmax()
+
+
+def test_qwen05b_int8_greedy_after_a_512_token_prompt_matches_the_oracle():
+    """The benchmark configuration's shape: 0.5B int8-g64 (clip search), a 512-token prompt
+    (four prefill chunks), then greedy decoding and speculative decoding with scripted drafts."""
+    say("0.5B int8: build")
+    m = qwen05b((8, 64))
+    rng = np.random.default_rng(512)
+    prompt = rng.integers(0, 151936, 512).tolist()
+    n = 12
+    gm = gpu_model(m, max_ctx=1024)
+    gl = [gm.forward(prompt)]
+    for _ in range(n - 1):
+        gl.append(gm.forward([int(np.argmax(gl[-1]))]))
+    g = [int(np.argmax(x)) for x in gl]
+    say("0.5B int8: oracle")
+    cpu = cpu_model(m, max_ctx=1024)
+    cl = [cpu.forward(prompt)]
+    for i in range(n - 1):
+        cl.append(cpu.forward([g[i]]))
+    for i in range(n):
+        srt = np.sort(cl[i])
+        rel = np.max(np.abs(gl[i] - cl[i])) / np.max(np.abs(cl[i]))
+        say(f"pos {i}: rel {rel:.2e}, margin {srt[-1] - srt[-2]:.3e}")
+        assert rel <= 1e-3
+        assert int(np.argmax(cl[i])) == g[i], i
+    # speculation with scripted drafts reproduces greedy decoding exactly
+    d = LS.ScriptedDrafter(g, 0.6, 7, 151936)
+    got, st = LS.speculative_greedy(gpu_model(m, max_ctx=1024), d, prompt, n, 8)
+    assert got == g and st["target_passes"] < n
