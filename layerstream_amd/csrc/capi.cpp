@@ -386,20 +386,33 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
         need(y_dev, "output");
         ls::Format F = ls::Format::from(f);
         F.validate({cols});
-        if (F.is_bf16() && cols % 8 != 0) ls::fail("bf16 rows must hold a multiple of 8 values");
         if (t == 0 || t > 128) ls::fail("t must be between 1 and 128");
         hipStream_t s = static_cast<hipStream_t>(stream);
-        ls::DevBuf data(ls::devmat_data_bytes(F.bits, int(rows), int(cols)));
-        ls::DevBuf scales(std::max<size_t>(2, 2 * ls::devmat_scale_count(F.bits, F.group, int(rows), int(cols))));
-        HIPC(hipMemsetAsync(data.p, F.bits == 4 ? 0x88 : 0, data.n, s));
-        HIPC(hipMemsetAsync(scales.p, 0, scales.n, s));
-        ls::repack_rows_device(static_cast<const uint8_t*>(w_dev), F.bits, F.group, int(rows), int(cols), data.as<uint8_t>(),
-                               scales.as<uint16_t>(), 0, int(rows), s);
-        ls::DevMat W = ls::bind_mat(data.as<uint8_t>(), scales.as<uint16_t>(), F, int(rows), int(cols));
-        int S = ls::matvec_splits(W, 1);
-        ls::DevBuf part(size_t(S) * t * W.n_strips * ls::STRIP * 4);
-        ls::matvec(W, x_dev, int(cols), int(t), part.as<float>(), S, s);
-        ls::reduce_store(part.as<float>(), S, int(t), int(rows), W.n_strips * ls::STRIP, nullptr, y_dev, int(rows), s);
+        const ls::TMat shape = ls::tile_shape(F.bits, F.group, int(rows), int(cols));
+        ls::DevBuf data(ls::tile_data_bytes(shape));
+        ls::DevBuf scales(std::max<size_t>(16, ls::tile_scale_bytes(shape)));
+        const ls::TMat W = ls::tile_bind(shape, data.as<uint8_t>(), scales.as<uint16_t>());
+        ls::tile_clear(W, s);
+        ls::tile_repack(static_cast<const uint8_t*>(w_dev), int(rows), W, 0, int(rows), int(rows), s);
+        HIPC(hipMemsetAsync(y_dev, 0, t * rows * 4, s));
+        const size_t fb = size_t(ls::tile_kpad(int(cols))) / 32 * 3 * 1024;
+        ls::DevBuf frags(fb > 96 * 1024 ? fb : 0);
+        for (int i0 = 0; i0 < int(t); i0 += ls::FTOK) {
+            const int nt = std::min(ls::FTOK, int(t) - i0);
+            ls::FusedArgs a;
+            a.W = W;
+            a.x = x_dev;
+            a.ldx = int(cols);
+            a.i0 = i0;
+            a.nt = nt;
+            a.out = y_dev;
+            a.ldo = int(rows);
+            if (frags.p) {
+                ls::frag_build(x_dev, int(cols), i0, nt, int(cols), nullptr, 0.0f, frags.as<uint8_t>(), s);
+                a.frags = frags.as<uint8_t>();
+            }
+            ls::fused_residual(a, 16, s);
+        }
         HIPC(hipStreamSynchronize(s));
     });
 }

@@ -1,18 +1,5 @@
-// Device kernels of the speculative verify step, written for gfx950 (CDNA4, wave64).
-//
-// Weight-streaming matvec: one weight row per lane, a wavefront owns a strip of 64 rows and
-// reads its chunks as contiguous 1 KiB loads; the t input vectors are wave-uniform and reach
-// the lanes through scalar loads, so each weight byte is read once from HBM and used for all t
-// rows (the "k+1 drafts share one weight read" of src/kernels.rs:153-168). Dequantization
-// happens in registers: int8 by sign-extending convert, int4 nibbles (low nibble = weight j,
-// high nibble = weight j + group/2, stored +8: src/kernels.rs:70-92) by shift/mask, bf16 by
-// widening. Per-group scales multiply the group's partial sum (src/kernels.rs:53-92).
-//
-// Determinism and batch invariance: every output element is computed by one lane with a fixed
-// FMA sequence over its columns, K is split into ranges that depend only on the matrix shape,
-// and the split partial sums are added in split order. So row r of a t-token launch is bit
-// identical to the same row computed alone, which is what lets a verify pass stand in for
-// t single-token passes (src/spec.rs:8-11).
+// Small device kernels of the verify step for gfx950 (CDNA4, wave64): attention, greedy
+// acceptance and helpers. The weight-streaming kernels live in fused.hip.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -31,597 +18,121 @@ namespace ls {
     } while (0)
 
 // ---------------------------------------------------------------------------------------
-// Layout helpers
+// Causal GQA attention (src/model.rs:261-282), split over the context in chunks of ACH keys
+// (flash-decoding). The reference computes scores (q . k_j) * scale, a softmax (max,
+// exp(x - max), sum, * 1/sum) and sum_j p_j v_j over every cached position; here each chunk
+// yields (m, l, o) = (max score, sum of exp(s - m), sum of exp(s - m) v) and the combine
+// rescales the chunks in chunk order. Chunk boundaries depend only on key positions, so a
+// token's result does not depend on how many tokens share the launch.
 // ---------------------------------------------------------------------------------------
-static inline size_t data_bytes_per_row(int bits, int cols) { return bits == 16 ? size_t(cols) * 2 : size_t(cols) * bits / 8; }
+constexpr int ACH = 64;  // keys per chunk
+constexpr int ATQ = 16;  // query tokens per block
 
-int devmat_chunks(int bits, int cols) { return int((data_bytes_per_row(bits, cols) + 15) / 16); }
-
-size_t devmat_data_bytes(int bits, int rows, int cols) {
-    size_t strips = (size_t(rows) + STRIP - 1) / STRIP;
-    return strips * devmat_chunks(bits, cols) * STRIP * 16;
-}
-
-size_t devmat_scale_count(int bits, int group, int rows, int cols) {
-    if (bits == 16) return 0;
-    size_t strips = (size_t(rows) + STRIP - 1) / STRIP;
-    return strips * (cols / group) * STRIP;
-}
-
-static inline uint8_t pad_byte(int bits) { return bits == 4 ? 0x88 : 0x00; }
-
-void repack_rows_host(const uint8_t* raw, int bits, int group, int rows, int cols, uint8_t* data, uint16_t* scales,
-                      int row_off, int dest_rows) {
-    const size_t db = data_bytes_per_row(bits, cols);
-    const size_t rb = db + (bits == 16 ? 0 : size_t(cols / group) * 2);
-    const int n_chunks = devmat_chunks(bits, cols);
-    const int n_groups = bits == 16 ? 0 : cols / group;
-    (void)dest_rows;
-    for (int r = 0; r < rows; r++) {
-        const uint8_t* src = raw + size_t(r) * rb;
-        int dr = row_off + r, strip = dr / STRIP, lane = dr % STRIP;
-        for (int c = 0; c < n_chunks; c++) {
-            uint8_t* dst = data + ((size_t(strip) * n_chunks + c) * STRIP + lane) * 16;
-            size_t o = size_t(c) * 16, n = db - o < 16 ? db - o : 16;
-            std::memcpy(dst, src + o, n);
-            if (n < 16) std::memset(dst + n, pad_byte(bits), 16 - n);
-        }
-        for (int g = 0; g < n_groups; g++)
-            scales[(size_t(strip) * n_groups + g) * STRIP + lane] = uint16_t(src[db + 2 * g] | (src[db + 2 * g + 1] << 8));
-    }
-}
-
-__global__ void k_repack(const uint8_t* __restrict__ raw, int bits, int group, int rows, int cols, uint8_t* __restrict__ data,
-                         uint16_t* __restrict__ scales, int row_off) {
-    const int db = bits == 16 ? cols * 2 : cols * bits / 8;
-    const int n_groups = bits == 16 ? 0 : cols / group;
-    const int rb = db + n_groups * 2;
-    const int n_chunks = (db + 15) / 16;
-    const int r = blockIdx.x;
-    if (r >= rows) return;
-    const uint8_t* src = raw + size_t(r) * rb;
-    const int dr = row_off + r, strip = dr / STRIP, lane = dr % STRIP;
-    for (int c = threadIdx.x; c < n_chunks; c += blockDim.x) {
-        uint8_t* dst = data + ((size_t(strip) * n_chunks + c) * STRIP + lane) * 16;
-        for (int b = 0; b < 16; b++) {
-            int o = c * 16 + b;
-            dst[b] = o < db ? src[o] : (bits == 4 ? 0x88 : 0);
-        }
-    }
-    for (int g = threadIdx.x; g < n_groups; g += blockDim.x)
-        scales[(size_t(strip) * n_groups + g) * STRIP + lane] = uint16_t(src[db + 2 * g] | (src[db + 2 * g + 1] << 8));
-}
-
-void repack_rows_device(const uint8_t* raw, int bits, int group, int rows, int cols, uint8_t* data, uint16_t* scales,
-                        int row_off, int dest_rows, hipStream_t s) {
-    (void)dest_rows;
-    if (rows == 0) return;
-    hipLaunchKernelGGL(k_repack, dim3(rows), dim3(64), 0, s, raw, bits, group, rows, cols, data, scales, row_off);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// Decoding one 16-byte chunk
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float bf16f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
-
-// int8: 16 weights in 4 dwords, little endian.
-__device__ __forceinline__ void dec_q8(const uint4& v, float* w) {
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) w[4 * k + b] = float(int32_t(d[k] << (24 - 8 * b)) >> 24);
-    }
-}
-
-// int4: 16 bytes -> 16 low-nibble weights (lo) and 16 high-nibble weights (hi), value - 8.
-__device__ __forceinline__ void dec_q4(const uint4& v, float* lo, float* hi) {
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            uint32_t byte = (d[k] >> (8 * b)) & 0xffu;
-            lo[4 * k + b] = float(int32_t(byte & 15u) - 8);
-            hi[4 * k + b] = float(int32_t(byte >> 4) - 8);
-        }
-    }
-}
-
-__device__ __forceinline__ void dec_bf16(const uint4& v, float* w) {
-    const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        w[2 * k] = __uint_as_float(d[k] << 16);
-        w[2 * k + 1] = __uint_as_float(d[k] & 0xffff0000u);
-    }
-}
-
-// acc[tt] += sum_k w[k] * x[tt][col + k] for k < N (x wave-uniform).
-template <int TT, int N>
-__device__ __forceinline__ void fma_run(float* acc, const float* w, const float* __restrict__ x, int ldx, int col) {
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) {
-        const float* xr = x + size_t(tt) * ldx + col;
-        float a = acc[tt];
-#pragma unroll
-        for (int k = 0; k < N; k++) a = __builtin_fmaf(w[k], xr[k], a);
-        acc[tt] = a;
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// Matvec. KIND 0 = bf16 (unit = chunk of 8 weights), 1 = int8 (unit = group), 2 = int4 with
-// group >= 32 (unit = group), 3 = int4 with group 16 (unit = chunk = two groups).
-// Block = 4 wavefronts = 4 strips; blockIdx.y = K split.
-// ---------------------------------------------------------------------------------------
-template <int KIND, int TT>
-__global__ __launch_bounds__(256) void k_matvec(const uint8_t* __restrict__ data, const uint16_t* __restrict__ scales,
-                                                int n_strips, int n_chunks, int n_groups, int group, int cols,
-                                                const float* __restrict__ x, int ldx, float* __restrict__ part,
-                                                int t_total, int t_off, int rows_pad, int units_per_split, int n_units) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int strip = blockIdx.x * 4 + wave;
-    if (strip >= n_strips) return;
-    const int split = blockIdx.y;
-    const int u0 = split * units_per_split;
-    const int u1 = min(n_units, u0 + units_per_split);
-    const uint8_t* base = data + (size_t(strip) * n_chunks * STRIP + lane) * 16;
-    float total[TT];
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) total[tt] = 0.0f;
-
-    if constexpr (KIND == 0) {
-        for (int c = u0; c < u1; c++) {
-            uint4 v = *reinterpret_cast<const uint4*>(base + size_t(c) * STRIP * 16);
-            float w[8];
-            dec_bf16(v, w);
-            fma_run<TT, 8>(total, w, x, ldx, c * 8);
-        }
-    } else if constexpr (KIND == 1) {
-        const int cpg = group / 16;
-        for (int g = u0; g < u1; g++) {
-            float acc[TT];
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) acc[tt] = 0.0f;
-            for (int j = 0; j < cpg; j++) {
-                int c = g * cpg + j;
-                uint4 v = *reinterpret_cast<const uint4*>(base + size_t(c) * STRIP * 16);
-                float w[16];
-                dec_q8(v, w);
-                fma_run<TT, 16>(acc, w, x, ldx, c * 16);
-            }
-            float s = bf16f(scales[(size_t(strip) * n_groups + g) * STRIP + lane]);
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) total[tt] = __builtin_fmaf(s, acc[tt], total[tt]);
-        }
-    } else if constexpr (KIND == 2) {
-        const int half = group / 2, cpg = half / 16;
-        for (int g = u0; g < u1; g++) {
-            float acc[TT];
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) acc[tt] = 0.0f;
-            for (int j = 0; j < cpg; j++) {
-                int c = g * cpg + j;
-                uint4 v = *reinterpret_cast<const uint4*>(base + size_t(c) * STRIP * 16);
-                float lo[16], hi[16];
-                dec_q4(v, lo, hi);
-                int col = g * group + j * 16;
-                fma_run<TT, 16>(acc, lo, x, ldx, col);
-                fma_run<TT, 16>(acc, hi, x, ldx, col + half);
-            }
-            float s = bf16f(scales[(size_t(strip) * n_groups + g) * STRIP + lane]);
-#pragma unroll
-            for (int tt = 0; tt < TT; tt++) total[tt] = __builtin_fmaf(s, acc[tt], total[tt]);
-        }
-    } else {
-        for (int c = u0; c < u1; c++) {
-            uint4 v = *reinterpret_cast<const uint4*>(base + size_t(c) * STRIP * 16);
-            float lo[16], hi[16];
-            dec_q4(v, lo, hi);
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                int g = 2 * c + h;
-                if (g >= n_groups) break;
-                float acc[TT];
-#pragma unroll
-                for (int tt = 0; tt < TT; tt++) acc[tt] = 0.0f;
-                fma_run<TT, 8>(acc, lo + 8 * h, x, ldx, g * 16);
-                fma_run<TT, 8>(acc, hi + 8 * h, x, ldx, g * 16 + 8);
-                float s = bf16f(scales[(size_t(strip) * n_groups + g) * STRIP + lane]);
-#pragma unroll
-                for (int tt = 0; tt < TT; tt++) total[tt] = __builtin_fmaf(s, acc[tt], total[tt]);
-            }
-        }
-    }
-    const int r = strip * STRIP + lane;
-#pragma unroll
-    for (int tt = 0; tt < TT; tt++) part[(size_t(split) * t_total + t_off + tt) * rows_pad + r] = total[tt];
-}
-
-static int mat_kind(const DevMat& W) {
-    if (W.bits == 16) return 0;
-    if (W.bits == 8) return 1;
-    return W.group >= 32 ? 2 : 3;
-}
-
-static int mat_units(const DevMat& W) {
-    switch (mat_kind(W)) {
-        case 1: case 2: return W.n_groups;
-        default: return W.n_chunks;
-    }
-}
-
-// The K split depends only on the matrix (never on t), so results do not depend on t.
-int matvec_splits(const DevMat& W, int) {
-    const int units = mat_units(W);
-    const int want_waves = 2048;
-    int splits = (want_waves + W.n_strips - 1) / W.n_strips;
-    if (splits < 1) splits = 1;
-    if (splits > units) splits = units;
-    int ups = (units + splits - 1) / splits;
-    return (units + ups - 1) / ups;
-}
-
-template <int KIND>
-static void launch_kind(const DevMat& W, const float* x, int ldx, int tt, float* part, int t_total, int t_off, int splits,
-                        int ups, int units, hipStream_t s) {
-    dim3 grid((W.n_strips + 3) / 4, splits), block(256);
-    const int rows_pad = W.n_strips * STRIP;
-#define LS_MV_CASE(N)                                                                                                   \
-    case N:                                                                                                             \
-        hipLaunchKernelGGL((k_matvec<KIND, N>), grid, block, 0, s, W.data, W.scales, W.n_strips, W.n_chunks, W.n_groups, \
-                           W.group, W.cols, x, ldx, part, t_total, t_off, rows_pad, ups, units);                        \
-        break;
-    switch (tt) {
-        LS_MV_CASE(1) LS_MV_CASE(2) LS_MV_CASE(3) LS_MV_CASE(4) LS_MV_CASE(5) LS_MV_CASE(6) LS_MV_CASE(7) LS_MV_CASE(8)
-        LS_MV_CASE(9) LS_MV_CASE(10) LS_MV_CASE(11) LS_MV_CASE(12) LS_MV_CASE(13) LS_MV_CASE(14) LS_MV_CASE(15) LS_MV_CASE(16)
-        default: throw std::runtime_error("matvec tile out of range");
-    }
-#undef LS_MV_CASE
-}
-
-void matvec(const DevMat& W, const float* x, int ldx, int t, float* part, int splits, hipStream_t s) {
-    const int units = mat_units(W);
-    const int ups = (units + splits - 1) / splits;
-    for (int t0 = 0; t0 < t; t0 += MAX_T) {
-        int tt = t - t0 < MAX_T ? t - t0 : MAX_T;
-        const float* xt = x + size_t(t0) * ldx;
-        switch (mat_kind(W)) {
-            case 0: launch_kind<0>(W, xt, ldx, tt, part, t, t0, splits, ups, units, s); break;
-            case 1: launch_kind<1>(W, xt, ldx, tt, part, t, t0, splits, ups, units, s); break;
-            case 2: launch_kind<2>(W, xt, ldx, tt, part, t, t0, splits, ups, units, s); break;
-            default: launch_kind<3>(W, xt, ldx, tt, part, t, t0, splits, ups, units, s); break;
-        }
-        HIPCHECK(hipGetLastError());
-    }
-}
-
-// ---------------------------------------------------------------------------------------
-// Epilogues over split partial sums
-// ---------------------------------------------------------------------------------------
-__global__ void k_reduce_store(const float* __restrict__ part, int splits, int t, int rows, int rows_pad,
-                               const float* __restrict__ bias, float* __restrict__ out, int ldo) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    const int tt = blockIdx.y;
-    if (r >= rows) return;
-    float v = part[size_t(tt) * rows_pad + r];
-    for (int sp = 1; sp < splits; sp++) v += part[(size_t(sp) * t + tt) * rows_pad + r];
-    if (bias) v += bias[r];
-    out[size_t(tt) * ldo + r] = v;
-}
-
-__global__ void k_reduce_residual(const float* __restrict__ part, int splits, int t, int rows, int rows_pad,
-                                  float* __restrict__ x, int ldx) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    const int tt = blockIdx.y;
-    if (r >= rows) return;
-    float v = part[size_t(tt) * rows_pad + r];
-    for (int sp = 1; sp < splits; sp++) v += part[(size_t(sp) * t + tt) * rows_pad + r];
-    x[size_t(tt) * ldx + r] += v;
-}
-
-void reduce_store(const float* part, int splits, int t, int rows, int rows_pad, const float* bias, float* out, int ldo,
-                  hipStream_t s) {
-    hipLaunchKernelGGL(k_reduce_store, dim3((rows + 255) / 256, t), dim3(256), 0, s, part, splits, t, rows, rows_pad, bias,
-                       out, ldo);
-    HIPCHECK(hipGetLastError());
-}
-
-void reduce_residual(const float* part, int splits, int t, int rows, int rows_pad, float* x, int ldx, hipStream_t s) {
-    hipLaunchKernelGGL(k_reduce_residual, dim3((rows + 255) / 256, t), dim3(256), 0, s, part, splits, t, rows, rows_pad,
-                       x, ldx);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// Embedding gather (src/kernels.rs:95-121 dequant_row: q * s, (nibble - 8) * s, bf16 widen)
-// ---------------------------------------------------------------------------------------
-__global__ void k_embed_gather(const uint8_t* __restrict__ data, const uint16_t* __restrict__ scales, int bits, int group,
-                               int cols, int n_chunks, int n_groups, const uint32_t* __restrict__ tokens,
-                               float* __restrict__ x) {
-    const int i = blockIdx.x;
-    const uint32_t row = tokens[i];
-    const int strip = row / STRIP, lane = row % STRIP;
-    float* out = x + size_t(i) * cols;
-    for (int c = threadIdx.x; c < n_chunks; c += blockDim.x) {
-        uint4 v = *reinterpret_cast<const uint4*>(data + ((size_t(strip) * n_chunks + c) * STRIP + lane) * 16);
-        if (bits == 16) {
-            float w[8];
-            dec_bf16(v, w);
-            for (int k = 0; k < 8; k++)
-                if (c * 8 + k < cols) out[c * 8 + k] = w[k];
-        } else if (bits == 8) {
-            float w[16];
-            dec_q8(v, w);
-            float s = bf16f(scales[(size_t(strip) * n_groups + (c * 16) / group) * STRIP + lane]);
-            for (int k = 0; k < 16; k++)
-                if (c * 16 + k < cols) out[c * 16 + k] = w[k] * s;
-        } else {
-            float lo[16], hi[16];
-            dec_q4(v, lo, hi);
-            const int half = group / 2;
-            for (int b = 0; b < 16; b++) {
-                int j = c * 16 + b;  // byte index within the row data
-                int g = j / half, jj = j % half;
-                if (g >= n_groups) break;
-                float s = bf16f(scales[(size_t(strip) * n_groups + g) * STRIP + lane]);
-                out[g * group + jj] = lo[b] * s;
-                out[g * group + half + jj] = hi[b] * s;
-            }
-        }
-    }
-}
-
-void embed_gather(const DevMat& E, const uint32_t* tokens, int t, float* x, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed_gather, dim3(t), dim3(64), 0, s, E.data, E.scales, E.bits, E.group, E.cols, E.n_chunks,
-                       E.n_groups, tokens, x);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// Block reductions (fixed order: lane sums via shuffles, then wavefronts in order)
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-// Sum over a block of 256 threads; every thread gets the result.
-__device__ float block_sum256(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float r = ((red[0] + red[1]) + red[2]) + red[3];
-    __syncthreads();
-    return r;
-}
-
-__device__ float block_max256(float v, float* red) {
-    v = wave_max(v);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    return r;
-}
-
-// ---------------------------------------------------------------------------------------
-// RMSNorm (src/kernels.rs:217-238): (x * inv) * w with inv = 1 / sqrt(mean(x^2) + eps)
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x, const float* __restrict__ w, int n, float eps,
-                                                  float* __restrict__ out) {
-    __shared__ float red[4];
-    const float* xr = x + size_t(blockIdx.x) * n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
-    ss = block_sum256(ss, red);
-    const float inv = 1.0f / sqrtf(ss / float(n) + eps);
-    float* o = out + size_t(blockIdx.x) * n;
-    for (int i = threadIdx.x; i < n; i += 256) o[i] = __fmul_rn(__fmul_rn(xr[i], inv), w[i]);
-}
-
-void rms_norm(const float* x, const float* w, int n, float eps, int t, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_rms_norm, dim3(t), dim3(256), 0, s, x, w, n, eps, out);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// RoPE + KV append (src/model.rs:249-259, src/kernels.rs:242-252)
-// ---------------------------------------------------------------------------------------
-__global__ void k_rope_append(float* __restrict__ qkv, int heads, int kv_heads, int hd, int pos0,
-                              const float* __restrict__ cos_t, const float* __restrict__ sin_t, float* __restrict__ kc,
-                              float* __restrict__ vc) {
-    const int i = blockIdx.x, pos = pos0 + i;
-    const int h = heads * hd, kv = kv_heads * hd, half = hd / 2;
-    float* row = qkv + size_t(i) * (h + 2 * kv);
-    const float* ct = cos_t + size_t(pos) * half;
-    const float* st = sin_t + size_t(pos) * half;
-    const int pairs = (heads + kv_heads) * half;
-    for (int p = threadIdx.x; p < pairs; p += blockDim.x) {
-        int head = p / half, j = p % half;
-        float* v = row + head * hd;  // q heads then k heads are adjacent in qkv
-        float a = v[j], b = v[j + half], c = ct[j], s = st[j];
-        v[j] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-        v[j + half] = __fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s));
-    }
-    __syncthreads();
-    for (int d = threadIdx.x; d < kv; d += blockDim.x) {
-        kc[size_t(pos) * kv + d] = row[h + d];
-        vc[size_t(pos) * kv + d] = row[h + kv + d];
-    }
-}
-
-void rope_append_kv(float* qkv, int t, int heads, int kv_heads, int hd, int pos0, const float* cos_t, const float* sin_t,
-                    float* k_cache, float* v_cache, hipStream_t s) {
-    hipLaunchKernelGGL(k_rope_append, dim3(t), dim3(256), 0, s, qkv, heads, kv_heads, hd, pos0, cos_t, sin_t, k_cache, v_cache);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// Causal GQA attention (src/model.rs:261-282): scores = (q . k_j) * scale, softmax
-// (max, exp(x - max), sum, * 1/sum), out = sum_j p_j v_j. One block per (token, head).
-// ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ qkv, int heads, int kv_heads, int hd, int pos0,
-                                                   int max_ctx, float scale, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, float* __restrict__ scores,
-                                                   float* __restrict__ out) {
-    __shared__ float q[256];
-    __shared__ float red[4];
-    __shared__ float accum[256];
-    const int i = blockIdx.x, head = blockIdx.y;
-    const int h = heads * hd, kv = kv_heads * hd;
+__global__ __launch_bounds__(256) void k_attn_chunk(const float* __restrict__ q, int ldq, int t, int heads, int kv_heads, int hd,
+                                                    int pos0, float scale, const float* __restrict__ kc,
+                                                    const float* __restrict__ vc, int nc_max, float* __restrict__ pm,
+                                                    float* __restrict__ pl, float* __restrict__ po) {
+    extern __shared__ float sm[];
+    const int c = blockIdx.x, head = blockIdx.y, i0 = blockIdx.z * ATQ;
+    const int kv = kv_heads * hd;
     const int g = head / (heads / kv_heads);
-    const int ctx = pos0 + i + 1;
-    const float* qr = qkv + size_t(i) * (h + 2 * kv) + head * hd;
-    for (int d = threadIdx.x; d < hd; d += 256) q[d] = qr[d];
+    const int j0 = c * ACH;
+    const int nq = min(ATQ, t - i0);
+    const int nk = min(ACH, pos0 + t - j0);  // keys that exist in this chunk
+    float* Ks = sm;                       // [ACH][hd + 1]
+    float* Vs = Ks + ACH * (hd + 1);      // [ACH][hd]
+    float* Q = Vs + ACH * hd;             // [ATQ][hd]
+    float* S = Q + ATQ * hd;              // [ATQ][ACH]
+    for (int p = threadIdx.x; p < ACH * hd; p += 256) {
+        const int j = p / hd, d = p % hd;
+        float kx = 0.0f, vx = 0.0f;
+        if (j < nk) {
+            kx = kc[size_t(j0 + j) * kv + g * hd + d];
+            vx = vc[size_t(j0 + j) * kv + g * hd + d];
+        }
+        Ks[j * (hd + 1) + d] = kx;
+        Vs[j * hd + d] = vx;
+    }
+    for (int p = threadIdx.x; p < nq * hd; p += 256) {
+        const int i = p / hd, d = p % hd;
+        Q[i * hd + d] = q[size_t(i0 + i) * ldq + head * hd + d];
+    }
     __syncthreads();
-    float* sc = scores + (size_t(i) * heads + head) * max_ctx;
-    float mx = -INFINITY;
-    for (int j = threadIdx.x; j < ctx; j += 256) {
-        const float* kr = kc + size_t(j) * kv + g * hd;
-        float s = 0.0f;
-        for (int d = 0; d < hd; d++) s = __builtin_fmaf(q[d], kr[d], s);
-        s *= scale;
-        sc[j] = s;
-        mx = fmaxf(mx, s);
+    for (int p = threadIdx.x; p < nq * ACH; p += 256) {
+        const int i = p / ACH, j = p % ACH;
+        float sc = -INFINITY;
+        if (j < nk && j0 + j <= pos0 + i0 + i) {
+            float a = 0.0f;
+            for (int d = 0; d < hd; d++) a = __builtin_fmaf(Q[i * hd + d], Ks[j * (hd + 1) + d], a);
+            sc = a * scale;
+        }
+        S[i * ACH + j] = sc;
     }
-    mx = block_max256(mx, red);
-    float sum = 0.0f;
-    for (int j = threadIdx.x; j < ctx; j += 256) {
-        float e = expf(sc[j] - mx);
-        sc[j] = e;
-        sum += e;
-    }
-    sum = block_sum256(sum, red);
-    const float inv = 1.0f / sum;
     __syncthreads();
-    const int parts = 256 / hd;  // hd divides 256 for hd in {16, 32, 64, 128, 256}
-    const int d = threadIdx.x % hd, part = threadIdx.x / hd;
-    float o = 0.0f;
-    if (part < parts) {
-        for (int j = part; j < ctx; j += parts) o = __builtin_fmaf(sc[j] * inv, vc[size_t(j) * kv + g * hd + d], o);
-    }
-    accum[threadIdx.x] = o;
-    __syncthreads();
-    if (threadIdx.x < hd) {
-        float r = accum[threadIdx.x];
-        for (int p = 1; p < parts; p++) r += accum[p * hd + threadIdx.x];
-        out[size_t(i) * h + head * hd + threadIdx.x] = r;
-    }
-}
-
-void attention(const float* qkv, int t, int heads, int kv_heads, int hd, int pos0, int max_ctx, const float* k_cache,
-               const float* v_cache, float* scores, float* out, hipStream_t s) {
-    if (hd > 256 || 256 % hd != 0) throw std::runtime_error("head_dim must divide 256");
-    const float scale = 1.0f / sqrtf(float(hd));
-    hipLaunchKernelGGL(k_attention, dim3(t, heads), dim3(256), 0, s, qkv, heads, kv_heads, hd, pos0, max_ctx, scale, k_cache,
-                       v_cache, scores, out);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// SwiGLU (src/model.rs:292-294, src/kernels.rs:268-270): silu(g) * u, silu(x) = x / (1 + e^-x)
-// ---------------------------------------------------------------------------------------
-__global__ void k_silu_mul(const float* __restrict__ gu, int inter, float* __restrict__ act) {
-    const int tt = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= inter) return;
-    const float g = gu[size_t(tt) * 2 * inter + i], u = gu[size_t(tt) * 2 * inter + inter + i];
-    act[size_t(tt) * inter + i] = __fmul_rn(g / (1.0f + expf(-g)), u);
-}
-
-void silu_mul(const float* gu, int t, int inter, float* act, hipStream_t s) {
-    hipLaunchKernelGGL(k_silu_mul, dim3((inter + 255) / 256, t), dim3(256), 0, s, gu, inter, act);
-    HIPCHECK(hipGetLastError());
-}
-
-// ---------------------------------------------------------------------------------------
-// Argmax with the reference's rule (src/spec.rs:41-49): the first index of the maximum; a
-// NaN never wins unless it sits at index 0 (then the answer is 0). As an order: non-NaN
-// before NaN, larger value first, lower index first; any reduction tree gives its minimum.
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
-    const bool an = isnan(va), bn = isnan(vb);
-    if (an != bn) return !an;
-    if (an) return ia < ib;
-    if (va != vb) return va > vb;
-    return ia < ib;
-}
-
-__device__ __forceinline__ void wave_argbest(float& v, int& ix) {
+    // One wavefront per query row: lane j holds key j (ACH == 64 == wave size).
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int i = w; i < nq; i += 4) {
+        const float sc = S[i * ACH + lane];
+        float m = sc;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(v, o, 64);
-        int oi = __shfl_xor(ix, o, 64);
-        if (beats(ov, oi, v, ix)) {
-            v = ov;
-            ix = oi;
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float e = sc == -INFINITY ? 0.0f : expf(sc - m);
+        float l = e;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+        S[i * ACH + lane] = e;
+        if (lane == 0) {
+            const size_t at = (size_t(i0 + i) * heads + head) * nc_max + c;
+            pm[at] = m;
+            pl[at] = l;
         }
-    }
-}
-
-constexpr int ARGMAX_BLOCKS = 64;
-
-__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ logits, int ld, int n, float* pval, int* pidx) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int row = blockIdx.y, b = blockIdx.x;
-    const float* lr = logits + size_t(row) * ld;
-    const int per = (n + ARGMAX_BLOCKS - 1) / ARGMAX_BLOCKS;
-    const int lo = b * per, hi = min(n, lo + per);
-    float v = NAN;
-    int ix = 0x7fffffff;
-    for (int i = lo + threadIdx.x; i < hi; i += 256) {
-        float x = lr[i];
-        if (beats(x, i, v, ix)) {
-            v = x;
-            ix = i;
-        }
-    }
-    wave_argbest(v, ix);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        sv[w] = v;
-        si[w] = ix;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float bv = sv[0];
-        int bi = si[0];
-        for (int k = 1; k < 4; k++)
-            if (beats(sv[k], si[k], bv, bi)) {
-                bv = sv[k];
-                bi = si[k];
-            }
-        pval[row * ARGMAX_BLOCKS + b] = bv;
-        pidx[row * ARGMAX_BLOCKS + b] = bi;
+    for (int p = threadIdx.x; p < nq * hd; p += 256) {
+        const int i = p / hd, d = p % hd;
+        float o = 0.0f;
+        for (int j = 0; j < ACH; j++) o = __builtin_fmaf(S[i * ACH + j], Vs[j * hd + d], o);
+        po[((size_t(i0 + i) * heads + head) * nc_max + c) * hd + d] = o;
     }
 }
 
-__global__ void k_argmax_final(const float* __restrict__ logits, int ld, const float* pval, const int* pidx, uint32_t* amax) {
-    const int row = blockIdx.x;
-    float v = pval[row * ARGMAX_BLOCKS + threadIdx.x];
-    int ix = pidx[row * ARGMAX_BLOCKS + threadIdx.x];
-    wave_argbest(v, ix);
-    if (threadIdx.x == 0) amax[row] = isnan(logits[size_t(row) * ld]) ? 0u : uint32_t(ix);
+// out[i][head] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M) over the chunks token i sees.
+__global__ void k_attn_combine(int heads, int hd, int pos0, int nc_max, const float* __restrict__ pm,
+                               const float* __restrict__ pl, const float* __restrict__ po, float* __restrict__ out) {
+    const int i = blockIdx.x, head = blockIdx.y;
+    const int nci = (pos0 + i + 1 + ACH - 1) / ACH;
+    const size_t base = (size_t(i) * heads + head) * nc_max;
+    float M = -INFINITY;
+    for (int c = 0; c < nci; c++) M = fmaxf(M, pm[base + c]);
+    float L = 0.0f;
+    for (int c = 0; c < nci; c++) L += pl[base + c] * expf(pm[base + c] - M);
+    const float inv = 1.0f / L;
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+        float o = 0.0f;
+        for (int c = 0; c < nci; c++) o = __builtin_fmaf(po[(base + c) * hd + d], expf(pm[base + c] - M), o);
+        out[size_t(i) * heads * hd + head * hd + d] = o * inv;
+    }
 }
 
-void argmax_rows(const float* logits, int ld, int n, int rows, float* pval, int* pidx, uint32_t* amax, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_part, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, s, logits, ld, n, pval, pidx);
+size_t attention_scratch_floats(int t, int heads, int hd, int max_ctx) {
+    const size_t nc = (size_t(max_ctx) + ACH - 1) / ACH;
+    return size_t(t) * heads * nc * (hd + 2);
+}
+
+void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, int pos0, int max_ctx, const float* k_cache,
+               const float* v_cache, float* scratch, float* out, hipStream_t s) {
+    if (hd > 256) throw std::runtime_error("head_dim too large");
+    const float scale = 1.0f / sqrtf(float(hd));
+    const int nc_max = (max_ctx + ACH - 1) / ACH;
+    const int nc = (pos0 + t + ACH - 1) / ACH;
+    float* pm = scratch;
+    float* pl = pm + size_t(t) * heads * nc_max;
+    float* po = pl + size_t(t) * heads * nc_max;
+    const size_t lds = sizeof(float) * (ACH * (hd + 1) + ACH * hd + ATQ * hd + ATQ * ACH);
+    hipLaunchKernelGGL(k_attn_chunk, dim3(nc, heads, (t + ATQ - 1) / ATQ), dim3(256), lds, s, q, ldq, t, heads, kv_heads, hd, pos0,
+                       scale, k_cache, v_cache, nc_max, pm, pl, po);
     HIPCHECK(hipGetLastError());
-    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(ARGMAX_BLOCKS), 0, s, logits, ld, pval, pidx, amax);
+    hipLaunchKernelGGL(k_attn_combine, dim3(t, heads), dim3(64), 0, s, heads, hd, pos0, nc_max, pm, pl, po, out);
     HIPCHECK(hipGetLastError());
 }
 

@@ -1,10 +1,17 @@
 // The device Model (src/model.rs) and its providers (src/provider.rs) on one MI355X.
 //
 // HBM layout: per layer one arena holding the fused q|k|v matrix, o, the fused gate|up matrix
-// and down in the strip layout (kernels.hpp), then the q|k|v bias and the two RMSNorm weight
-// vectors as f32. The tied embedding table is one strip-layout matrix used both for the
-// embedding gather and as the output head. The KV cache is f32 [layer][max_ctx][kv_dim] for K
-// and for V, as the reference's (src/model.rs:67-68); rollback is O(1) (only `pos` moves).
+// (64-row blocks of gate and up interleaved) and down in the tile layout (fused.hpp), then the
+// q|k|v bias and the two RMSNorm weight vectors as f32. The tied embedding table is one
+// tile-layout matrix used both for the embedding gather and as the output head. The KV cache is
+// f32 [layer][max_ctx][kv_dim] for K and for V, as the reference's (src/model.rs:67-68);
+// rollback is O(1) (only `pos` moves).
+//
+// A forward pass over t tokens runs per layer: fused QKV (RMSNorm prologue, bias + RoPE + K/V
+// append epilogue), chunked attention and its combine, fused O projection (+ residual), fused
+// gate|up (RMSNorm prologue, SiLU(g) * u epilogue into B fragments) and fused down (+ residual),
+// each launched once per tile of 16 tokens; then the head (final RMSNorm prologue, per-block
+// argmax epilogue) and the argmax reduction.
 #include "model.hpp"
 
 #include <chrono>
@@ -52,83 +59,67 @@ PinnedBuf& PinnedBuf::operator=(PinnedBuf&& o) noexcept {
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-DevMat bind_mat(uint8_t* data, uint16_t* scales, const Format& f, int rows, int cols) {
-    DevMat m;
-    m.data = data;
-    m.scales = f.is_bf16() ? nullptr : scales;
-    m.bits = f.bits;
-    m.group = f.is_bf16() ? 0 : f.group;
-    m.rows = rows;
-    m.cols = cols;
-    m.n_strips = (rows + STRIP - 1) / STRIP;
-    m.n_chunks = devmat_chunks(f.bits, cols);
-    m.n_groups = f.is_bf16() ? 0 : cols / f.group;
-    return m;
-}
-
-static void mat_region(size_t& off, size_t& d, size_t& s, const Format& f, size_t rows, size_t cols) {
+static void mat_region(size_t& off, size_t& d, size_t& s, const TMat& m) {
     d = off;
-    off = align256(off + devmat_data_bytes(f.bits, int(rows), int(cols)));
+    off = align256(off + tile_data_bytes(m));
     s = off;
-    off = align256(off + 2 * devmat_scale_count(f.bits, f.group, int(rows), int(cols)));
+    off = align256(off + tile_scale_bytes(m));
 }
 
 LayerArena layer_arena(const Config& c) {
     LayerArena a{};
-    size_t off = 0, h = c.hidden, kv = c.kv_dim(), in = c.inter;
-    mat_region(off, a.qkv_d, a.qkv_s, c.format, h + 2 * kv, h);
-    mat_region(off, a.o_d, a.o_s, c.format, h, h);
-    mat_region(off, a.gu_d, a.gu_s, c.format, 2 * in, h);
-    mat_region(off, a.down_d, a.down_s, c.format, h, in);
+    const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter), b = c.format.bits, g = c.format.group;
+    a.qkv = tile_shape(b, g, h + 2 * kv, h);
+    a.o = tile_shape(b, g, h, h);
+    a.gu = tile_shape(b, g, 2 * in, h);
+    a.down = tile_shape(b, g, h, in);
+    size_t off = 0;
+    mat_region(off, a.qkv_d, a.qkv_s, a.qkv);
+    mat_region(off, a.o_d, a.o_s, a.o);
+    mat_region(off, a.gu_d, a.gu_s, a.gu);
+    mat_region(off, a.down_d, a.down_s, a.down);
     a.b_qkv = off;
-    off = align256(off + 4 * (h + 2 * kv));
+    off = align256(off + 4 * size_t(h + 2 * kv));
     a.in_norm = off;
-    off = align256(off + 4 * h);
+    off = align256(off + 4 * size_t(h));
     a.post_norm = off;
-    off = align256(off + 4 * h);
+    off = align256(off + 4 * size_t(h));
     a.total = off;
     return a;
 }
 
-DevLayer bind_layer(const Config& c, const LayerArena& a, uint8_t* b) {
+DevLayer bind_layer(const LayerArena& a, uint8_t* b) {
     DevLayer L;
-    int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter);
-    L.qkv = bind_mat(b + a.qkv_d, reinterpret_cast<uint16_t*>(b + a.qkv_s), c.format, h + 2 * kv, h);
-    L.o = bind_mat(b + a.o_d, reinterpret_cast<uint16_t*>(b + a.o_s), c.format, h, h);
-    L.gu = bind_mat(b + a.gu_d, reinterpret_cast<uint16_t*>(b + a.gu_s), c.format, 2 * in, h);
-    L.down = bind_mat(b + a.down_d, reinterpret_cast<uint16_t*>(b + a.down_s), c.format, h, in);
+    L.qkv = tile_bind(a.qkv, b + a.qkv_d, reinterpret_cast<uint16_t*>(b + a.qkv_s));
+    L.o = tile_bind(a.o, b + a.o_d, reinterpret_cast<uint16_t*>(b + a.o_s));
+    L.gu = tile_bind(a.gu, b + a.gu_d, reinterpret_cast<uint16_t*>(b + a.gu_s));
+    L.down = tile_bind(a.down, b + a.down_d, reinterpret_cast<uint16_t*>(b + a.down_s));
     L.b_qkv = reinterpret_cast<const float*>(b + a.b_qkv);
     L.in_norm = reinterpret_cast<const float*>(b + a.in_norm);
     L.post_norm = reinterpret_cast<const float*>(b + a.post_norm);
     return L;
 }
 
-// Fill the padding of every matrix of an arena: int4 padding bytes must decode to weight 0.
-static void init_arena(const Config& c, const LayerArena& a, uint8_t* b, hipStream_t s) {
+void clear_layer(const LayerArena& a, uint8_t* b, hipStream_t s) {
     HIPC(hipMemsetAsync(b, 0, a.total, s));
-    if (c.format.bits == 4) {
-        size_t h = c.hidden, kv = c.kv_dim(), in = c.inter;
-        HIPC(hipMemsetAsync(b + a.qkv_d, 0x88, devmat_data_bytes(4, int(h + 2 * kv), int(h)), s));
-        HIPC(hipMemsetAsync(b + a.o_d, 0x88, devmat_data_bytes(4, int(h), int(h)), s));
-        HIPC(hipMemsetAsync(b + a.gu_d, 0x88, devmat_data_bytes(4, int(2 * in), int(h)), s));
-        HIPC(hipMemsetAsync(b + a.down_d, 0x88, devmat_data_bytes(4, int(h), int(in)), s));
-    }
+    DevLayer L = bind_layer(a, b);
+    tile_clear(L.qkv, s);
+    tile_clear(L.o, s);
+    tile_clear(L.gu, s);
+    tile_clear(L.down, s);
 }
 
 void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* raw, const LayerArena& a, uint8_t* b,
                         hipStream_t s) {
-    const int bits = c.format.bits, g = c.format.group;
     const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter);
-    auto rp = [&](int slot, int rows, int cols, size_t d, size_t sc, int row_off) {
-        repack_rows_device(raw + L.off[slot], bits, g, rows, cols, b + d, reinterpret_cast<uint16_t*>(b + sc), row_off, 0, s);
-    };
-    rp(T_Q_W, h, h, a.qkv_d, a.qkv_s, 0);
-    rp(T_K_W, kv, h, a.qkv_d, a.qkv_s, h);
-    rp(T_V_W, kv, h, a.qkv_d, a.qkv_s, h + kv);
-    rp(T_O_W, h, h, a.o_d, a.o_s, 0);
-    rp(T_GATE, in, h, a.gu_d, a.gu_s, 0);
-    rp(T_UP, in, h, a.gu_d, a.gu_s, in);
-    rp(T_DOWN, h, in, a.down_d, a.down_s, 0);
+    const DevLayer D = bind_layer(a, b);
+    tile_repack(raw + L.off[T_Q_W], h, D.qkv, 0, h, h, s);
+    tile_repack(raw + L.off[T_K_W], kv, D.qkv, h, kv, kv, s);
+    tile_repack(raw + L.off[T_V_W], kv, D.qkv, h + kv, kv, kv, s);
+    tile_repack(raw + L.off[T_O_W], h, D.o, 0, h, h, s);
+    tile_repack(raw + L.off[T_GATE], in, D.gu, 0, 64, 128, s);
+    tile_repack(raw + L.off[T_UP], in, D.gu, 64, 64, 128, s);
+    tile_repack(raw + L.off[T_DOWN], h, D.down, 0, h, h, s);
     float* bq = reinterpret_cast<float*>(b + a.b_qkv);
     bf16_to_f32_dev(raw + L.off[T_Q_B], h, bq, s);
     bf16_to_f32_dev(raw + L.off[T_K_B], kv, bq + h, s);
@@ -151,29 +142,27 @@ public:
         DevBuf raw(stage_bytes);
         for (size_t l = 0; l < c_.layers; l++) {
             uint8_t* b = arena_.as<uint8_t>() + l * a_.total;
-            init_arena(c_, a_, b, s_);
+            clear_layer(a_, b, s_);
             src.read_layer(l, stage.as<uint8_t>());
             HIPC(hipMemcpyAsync(raw.p, stage.p, L.total, hipMemcpyHostToDevice, s_));
             build_layer_device(c_, L, raw.as<uint8_t>(), a_, b, s_);
             HIPC(hipStreamSynchronize(s_));
-            layers_.push_back(bind_layer(c_, a_, b));
+            layers_.push_back(bind_layer(a_, b));
         }
         const Format ef = c_.embed_format;
         const int V = int(c_.vocab), h = int(c_.hidden);
-        edata_ = DevBuf(devmat_data_bytes(ef.bits, V, h));
-        escales_ = DevBuf(std::max<size_t>(2, 2 * devmat_scale_count(ef.bits, ef.group, V, h)));
-        HIPC(hipMemsetAsync(edata_.p, ef.bits == 4 ? 0x88 : 0, edata_.n, s_));
-        HIPC(hipMemsetAsync(escales_.p, 0, escales_.n, s_));
+        const TMat shape = tile_shape(ef.bits, ef.group, V, h, 256);
+        edata_ = DevBuf(tile_data_bytes(shape));
+        escales_ = DevBuf(std::max<size_t>(16, tile_scale_bytes(shape)));
+        E_ = tile_bind(shape, edata_.as<uint8_t>(), escales_.as<uint16_t>());
+        tile_clear(E_, s_);
         for (size_t first = 0; first < c_.vocab; first += HEAD_ROWS) {
-            size_t rows = std::min(HEAD_ROWS, c_.vocab - first);
+            const size_t rows = std::min(HEAD_ROWS, c_.vocab - first);
             src.read_embed_rows(first, rows, stage.as<uint8_t>());
             HIPC(hipMemcpyAsync(raw.p, stage.p, rows * rb, hipMemcpyHostToDevice, s_));
-            repack_rows_device(raw.as<uint8_t>(), ef.bits, ef.group, int(rows), h, edata_.as<uint8_t>(), escales_.as<uint16_t>(),
-                               int(first), V, s_);
+            tile_repack(raw.as<uint8_t>(), int(rows), E_, int(first), int(rows), int(rows), s_);
             HIPC(hipStreamSynchronize(s_));
         }
-        E_ = bind_mat(edata_.as<uint8_t>(), escales_.as<uint16_t>(), ef, V, h);
-        head_splits = matvec_splits(E_, 1);
     }
     const char* name() const override { return "resident"; }
     void begin_forward(bool) override {}
@@ -189,7 +178,7 @@ public:
     }
     void release_head_chunk(size_t) override {}
     void end_forward() override {}
-    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x) override { embed_gather(E_, dev_tokens, t, x, s_); }
+    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x) override { tile_embed(E_, dev_tokens, t, x, s_); }
     ls_report report() const override {
         ls_report r{};
         r.resident_weight_bytes = arena_.n + edata_.n + escales_.n;
@@ -204,7 +193,7 @@ private:
     hipStream_t s_;
     DevBuf arena_, edata_, escales_;
     std::vector<DevLayer> layers_;
-    DevMat E_;
+    TMat E_;
 };
 
 // ---------------------------------------------------------------------------------------
@@ -237,25 +226,21 @@ public:
         const size_t rb = c_.row_bytes();
         buf_size_ = std::max(L_.total, std::min(HEAD_ROWS, c_.vocab) * rb);
         const Format ef = c_.embed_format;
-        const int h = int(c_.hidden);
+        hshape_ = tile_shape(ef.bits, ef.group, int(HEAD_ROWS), int(c_.hidden), 256);
         slots_.resize(size_t(slots));
         for (auto& s : slots_) {
             s.raw = DevBuf(buf_size_);
             s.arena = DevBuf(a_.total);
-            init_arena(c_, a_, s.arena.as<uint8_t>(), copy_);
-            s.hdata = DevBuf(devmat_data_bytes(ef.bits, int(HEAD_ROWS), h));
-            s.hscales = DevBuf(std::max<size_t>(2, 2 * devmat_scale_count(ef.bits, ef.group, int(HEAD_ROWS), h)));
-            HIPC(hipMemsetAsync(s.hdata.p, ef.bits == 4 ? 0x88 : 0, s.hdata.n, copy_));
-            HIPC(hipMemsetAsync(s.hscales.p, 0, s.hscales.n, copy_));
+            clear_layer(a_, s.arena.as<uint8_t>(), copy_);
+            s.hdata = DevBuf(tile_data_bytes(hshape_));
+            s.hscales = DevBuf(std::max<size_t>(16, tile_scale_bytes(hshape_)));
+            tile_clear(tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>()), copy_);
             if (!src_.pinned()) s.stage = PinnedBuf(buf_size_);
             HIPC(hipEventCreateWithFlags(&s.copied, hipEventDisableTiming));
             HIPC(hipEventCreateWithFlags(&s.ready, hipEventDisableTiming));
             HIPC(hipEventCreateWithFlags(&s.freed, hipEventDisableTiming));
         }
         HIPC(hipStreamSynchronize(copy_));
-        // The head's K split is the one of the whole table, so logits match the resident mode.
-        DevMat full = bind_mat(nullptr, nullptr, ef, int(c_.vocab), h);
-        head_splits = matvec_splits(full, 1);
         embed_stage_ = PinnedBuf(128 * rb);
         embed_raw_ = DevBuf(128 * rb);
         HIPC(hipEventCreateWithFlags(&embed_copied_, hipEventDisableTiming));
@@ -287,15 +272,17 @@ public:
 
     const DevLayer& layer(size_t l) override {
         Slot& s = take({LAYER, l});
-        cur_layer_ = bind_layer(c_, a_, s.arena.as<uint8_t>());
+        cur_layer_ = bind_layer(a_, s.arena.as<uint8_t>());
         return cur_layer_;
     }
     void release_layer(size_t) override { release(); }
     size_t n_head_chunks() const override { return (c_.vocab + HEAD_ROWS - 1) / HEAD_ROWS; }
     HeadChunk head_chunk(size_t c) override {
         Slot& s = take({HEAD, c});
-        size_t first = c * HEAD_ROWS, rows = std::min(HEAD_ROWS, c_.vocab - first);
-        return HeadChunk{first, rows, bind_mat(s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>(), c_.embed_format, int(rows), int(c_.hidden))};
+        const size_t first = c * HEAD_ROWS, rows = std::min(HEAD_ROWS, c_.vocab - first);
+        TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
+        m.rows = int(rows);
+        return HeadChunk{first, rows, m};
     }
     void release_head_chunk(size_t) override { release(); }
     void end_forward() override {
@@ -316,7 +303,6 @@ public:
 
     ls_report report() const override {
         ls_report r{};
-        r.resident_weight_bytes = 0;
         for (auto& s : slots_) r.resident_weight_bytes += s.raw.n + s.arena.n + s.hdata.n + s.hscales.n;
         r.bytes_read = src_.bytes_read();
         r.wait_ns = wait_ns_;
@@ -356,9 +342,8 @@ private:
         if (it.kind == LAYER) {
             build_layer_device(c_, L_, s.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), copy_);
         } else {
-            const Format ef = c_.embed_format;
-            repack_rows_device(s.raw.as<uint8_t>(), ef.bits, ef.group, int(rows), int(c_.hidden), s.hdata.as<uint8_t>(),
-                               s.hscales.as<uint16_t>(), 0, int(HEAD_ROWS), copy_);
+            TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
+            tile_repack(s.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), copy_);
         }
         HIPC(hipEventRecord(s.ready, copy_));
         s.used = true;
@@ -390,6 +375,7 @@ private:
     Config c_;
     LayerLayout L_;
     LayerArena a_;
+    TMat hshape_;
     hipStream_t compute_, copy_ = nullptr;
     std::vector<Slot> slots_;
     std::vector<Item> schedule_;
@@ -413,14 +399,16 @@ std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStr
 // Model
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
+constexpr size_t FRAG_LDS_LIMIT = 96 * 1024;
+constexpr int MAX_TILES = int(PREFILL_CHUNK) / FTOK;
 
 Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx) {
     if (max_ctx == 0) fail("max_ctx must be positive");
     const Config& c = cfg_;
-    if (c.embed_format.is_bf16() && c.hidden % 8 != 0) fail("bf16 rows must hold a multiple of 8 values");
-    if (c.format.is_bf16() && (c.hidden % 8 != 0 || c.inter % 8 != 0)) fail("bf16 rows must hold a multiple of 8 values");
+    if (c.inter % 64 != 0) fail("the intermediate size must be a multiple of 64");
     if (c.head_dim > 256 || 256 % c.head_dim != 0) fail("head_dim must divide 256");
+    if (c.head_dim > 64 && c.head_dim % 64 != 0) fail("head_dim above 64 must be a multiple of 64");
     HIPC(hipSetDevice(device));
     HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     HIPC(hipEventCreate(&ev0_));
@@ -454,37 +442,27 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     fnorm_ = DevBuf(h * 4);
     HIPC(hipMemcpy(fnorm_.p, src.final_norm().data(), h * 4, hipMemcpyHostToDevice));
 
-    // Split counts depend only on matrix shapes (so results never depend on t).
-    DevMat qkv = bind_mat(nullptr, nullptr, c.format, int(h + 2 * kv), int(h));
-    DevMat o = bind_mat(nullptr, nullptr, c.format, int(h), int(h));
-    DevMat gu = bind_mat(nullptr, nullptr, c.format, int(2 * in), int(h));
-    DevMat dn = bind_mat(nullptr, nullptr, c.format, int(h), int(in));
-    s_qkv_ = matvec_splits(qkv, 1);
-    s_o_ = matvec_splits(o, 1);
-    s_gu_ = matvec_splits(gu, 1);
-    s_down_ = matvec_splits(dn, 1);
-    auto rp = [](const DevMat& m) { return size_t(m.n_strips) * STRIP; };
-    vpad_ = (c.vocab + STRIP - 1) / STRIP * STRIP;
-    part_floats_ = std::max({s_qkv_ * rp(qkv), s_o_ * rp(o), s_gu_ * rp(gu), s_down_ * rp(dn),
-                             size_t(prov_->head_splits) * std::max(vpad_, HEAD_ROWS)}) * T;
-
+    vpad_ = (c.vocab + 63) / 64 * 64;
+    head_blocks_ = fused_head_blocks(tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256));
+    act_frag_bytes_ = size_t(tile_kpad(int(in))) / 32 * 3 * 1024;
     x_ = DevBuf(T * h * 4);
-    xn_ = DevBuf(T * h * 4);
-    qkv_ = DevBuf(T * (h + 2 * kv) * 4);
+    q_ = DevBuf(T * h * 4);
     attn_ = DevBuf(T * h * 4);
-    gu_ = DevBuf(T * 2 * in * 4);
-    act_ = DevBuf(T * in * 4);
-    part_ = DevBuf(part_floats_ * 4);
-    scores_ = DevBuf(T * c.heads * max_ctx * 4);
+    act_frags_ = DevBuf(act_frag_bytes_ * MAX_TILES);
+    HIPC(hipMemsetAsync(act_frags_.p, 0, act_frags_.n, stream_));  // padding columns stay zero
+    in_frags_ = DevBuf(size_t(tile_kpad(int(h))) / 32 * 3 * 1024);
+    head_frags_ = DevBuf(size_t(tile_kpad(int(h))) / 32 * 3 * 1024 * MAX_TILES);
+    attn_scratch_ = DevBuf(attention_scratch_floats(int(T), int(c.heads), int(c.head_dim), int(max_ctx)) * 4);
     logits_ = DevBuf(T * vpad_ * 4);
-    hf_ = DevBuf(T * h * 4);
+    hpv_ = DevBuf(size_t(MAX_TILES) * (head_blocks_ + 1) * FTOK * 4);
+    hpi_ = DevBuf(size_t(MAX_TILES) * (head_blocks_ + 1) * FTOK * 4);
     amax_ = DevBuf(T * 4);
-    pval_ = DevBuf(T * 64 * 4);
-    pidx_ = DevBuf(T * 64 * 4);
     tok_ = DevBuf(max_ctx * 4);
     acc_ = DevBuf(16);
+    pos_dev_ = DevBuf((max_ctx / PREFILL_CHUNK + 2) * 4);
     h_tok_ = PinnedBuf(max_ctx * 4);
     h_out_ = PinnedBuf(T * 4 + 16);
+    h_pos_ = PinnedBuf((max_ctx / PREFILL_CHUNK + 2) * 4);
     HIPC(hipStreamSynchronize(stream_));
 }
 
@@ -512,28 +490,27 @@ void Model::check_request(const uint32_t* tok, size_t n) const {
         if (tok[i] >= cfg_.vocab) fail("token id " + std::to_string(tok[i]) + " is outside the vocabulary");
 }
 
-// forward_chunk (src/model.rs:161-220), all on the compute stream.
-void Model::mv(const DevMat& W, const float* x, int ldx, int t, float* part, int splits) {
-    if (!prof_) {
-        matvec(W, x, ldx, t, part, splits, stream_);
-        return;
-    }
+// ---- profiling of the weight-streaming kernels ------------------------------------------
+void Model::prof_begin() {
+    if (!prof_) return;
     while (prof_ev_.size() < prof_used_ + 2) {
         hipEvent_t e;
         HIPC(hipEventCreate(&e));
         prof_ev_.push_back(e);
     }
     HIPC(hipEventRecord(prof_ev_[prof_used_], stream_));
-    matvec(W, x, ldx, t, part, splits, stream_);
+}
+
+void Model::prof_end(const TMat& W, int nt) {
+    if (!prof_) return;
     HIPC(hipEventRecord(prof_ev_[prof_used_ + 1], stream_));
     prof_used_ += 2;
     const Format f{W.bits, W.group};
     prof_acc_.launches++;
-    prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * t * (double(W.cols) + double(W.rows));
-    prof_acc_.flops += 2.0 * t * double(W.rows) * double(W.cols);
+    prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * nt * (double(W.cols) + double(W.rows));
+    prof_acc_.flops += 2.0 * nt * double(W.rows) * double(W.cols);
 }
 
-// Sum the device time of the profiled launches (called after the stream has drained).
 void Model::harvest() {
     for (size_t i = 0; i + 1 < prof_used_; i += 2) {
         float ms = 0;
@@ -558,66 +535,154 @@ ls_kernel_stat Model::read_profile() {
     return r;
 }
 
-void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits) {
+const uint8_t* Model::global_frags(const float* x, int i0, int nt, int cols, const float* w) {
+    if (size_t(tile_kpad(cols)) / 32 * 3 * 1024 <= FRAG_LDS_LIMIT) return nullptr;
+    frag_build(x, int(cfg_.hidden), i0, nt, cols, w, cfg_.eps, in_frags_.as<uint8_t>(), stream_);
+    return in_frags_.as<uint8_t>();
+}
+
+// Copy a call's tokens (and the position of each 128-token chunk) to the device once. The
+// pinned staging buffers are only rewritten by the next call, after this call has drained.
+const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
+    std::memcpy(h_tok_.p, tok, n * 4);
+    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
+    const size_t chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
+    for (size_t ci = 0; ci < chunks; ci++) h_pos_.as<int>()[ci] = int(pos_ + ci * PREFILL_CHUNK);
+    HIPC(hipMemcpyAsync(pos_dev_.p, h_pos_.p, chunks * 4, hipMemcpyHostToDevice, stream_));
+    return tok_.as<uint32_t>();
+}
+
+// forward_chunk (src/model.rs:161-220), all on the compute stream.
+void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits) {
     const Config& c = cfg_;
-    const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter), T = int(t);
+    const int h = int(c.hidden), kv = int(c.kv_dim()), T = int(t);
     const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim), pos0 = int(pos_);
     hipStream_t s = stream_;
     float* x = x_.as<float>();
-    float* xn = xn_.as<float>();
-    float* qkv = qkv_.as<float>();
-    float* part = part_.as<float>();
+    const int* pos_dev = pos_dev_.as<int>() + chunk_index_;  // this chunk's first position
     prov_->embed(tok, dtok, T, x);
     prov_->begin_forward(n_logits > 0);
     for (size_t l = 0; l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
         float* kc = kcache_.as<float>() + l * max_ctx_ * kv;
         float* vc = vcache_.as<float>() + l * max_ctx_ * kv;
-        rms_norm(x, L.in_norm, h, c.eps, T, xn, s);
-        mv(L.qkv, xn, h, T, part, s_qkv_);
-        reduce_store(part, s_qkv_, T, h + 2 * kv, L.qkv.n_strips * STRIP, L.b_qkv, qkv, h + 2 * kv, s);
-        rope_append_kv(qkv, T, heads, kvh, hd, pos0, rope_cos_.as<float>(), rope_sin_.as<float>(), kc, vc, s);
-        attention(qkv, T, heads, kvh, hd, pos0, int(max_ctx_), kc, vc, scores_.as<float>(), attn_.as<float>(), s);
-        mv(L.o, attn_.as<float>(), h, T, part, s_o_);
-        reduce_residual(part, s_o_, T, h, L.o.n_strips * STRIP, x, h, s);
-        rms_norm(x, L.post_norm, h, c.eps, T, xn, s);
-        mv(L.gu, xn, h, T, part, s_gu_);
-        reduce_store(part, s_gu_, T, 2 * in, L.gu.n_strips * STRIP, nullptr, gu_.as<float>(), 2 * in, s);
-        silu_mul(gu_.as<float>(), T, in, act_.as<float>(), s);
-        mv(L.down, act_.as<float>(), in, T, part, s_down_);
-        reduce_residual(part, s_down_, T, h, L.down.n_strips * STRIP, x, h, s);
+        for (int i0 = 0; i0 < T; i0 += FTOK) {
+            const int nt = std::min(FTOK, T - i0);
+            FusedArgs a;
+            a.W = L.qkv;
+            a.x = x;
+            a.ldx = h;
+            a.norm = L.in_norm;
+            a.eps = c.eps;
+            a.frags = global_frags(x, i0, nt, h, L.in_norm);
+            a.i0 = i0;
+            a.nt = nt;
+            a.bias = L.b_qkv;
+            a.out = q_.as<float>();
+            a.ldo = h;
+            a.kcache = kc;
+            a.vcache = vc;
+            a.rope_cos = rope_cos_.as<float>();
+            a.rope_sin = rope_sin_.as<float>();
+            a.pos0 = pos_dev;
+            a.heads = heads;
+            a.kv_heads = kvh;
+            a.hd = hd;
+            prof_begin();
+            fused_qkv(a, s);
+            prof_end(L.qkv, nt);
+        }
+        attention(q_.as<float>(), h, T, heads, kvh, hd, pos0, int(max_ctx_), kc, vc, attn_scratch_.as<float>(), attn_.as<float>(), s);
+        for (int i0 = 0; i0 < T; i0 += FTOK) {
+            const int nt = std::min(FTOK, T - i0);
+            FusedArgs a;
+            a.W = L.o;
+            a.x = attn_.as<float>();
+            a.ldx = h;
+            a.frags = global_frags(attn_.as<float>(), i0, nt, h, nullptr);
+            a.i0 = i0;
+            a.nt = nt;
+            a.out = x;
+            a.ldo = h;
+            prof_begin();
+            fused_residual(a, 16, s);
+            prof_end(L.o, nt);
+        }
+        for (int i0 = 0; i0 < T; i0 += FTOK) {
+            const int nt = std::min(FTOK, T - i0);
+            uint8_t* af = act_frags_.as<uint8_t>() + size_t(i0 / FTOK) * act_frag_bytes_;
+            FusedArgs a;
+            a.W = L.gu;
+            a.x = x;
+            a.ldx = h;
+            a.norm = L.post_norm;
+            a.eps = c.eps;
+            a.frags = global_frags(x, i0, nt, h, L.post_norm);
+            a.i0 = i0;
+            a.nt = nt;
+            a.frag_out = af;
+            prof_begin();
+            fused_gate_up(a, s);
+            prof_end(L.gu, nt);
+            FusedArgs d;
+            d.W = L.down;
+            d.frags = af;
+            d.i0 = i0;
+            d.nt = nt;
+            d.out = x;
+            d.ldo = h;
+            prof_begin();
+            fused_residual(d, 16, s);
+            prof_end(L.down, nt);
+        }
         prov_->release_layer(l);
     }
     if (n_logits > 0) {
-        // Head (src/model.rs:190-216): final RMSNorm of the last n rows, the tied table in
-        // chunks (one chunk when resident), then the per-row argmax on the device.
+        // Head (src/model.rs:190-216): final RMSNorm of the last n rows in the prologue, the tied
+        // table (one chunk when resident), per-block argmax partials, then the argmax.
         const int n = int(n_logits);
-        rms_norm(x + size_t(T - n) * h, fnorm_.as<float>(), h, c.eps, n, hf_.as<float>(), s);
+        const float* xh = x + size_t(T - n) * h;
         float* logits = logits_.as<float>();
-        const int S = prov_->head_splits;
+        const size_t tile_stride = size_t(head_blocks_ + 1) * FTOK;
+        const size_t fb = size_t(tile_kpad(h)) / 32 * 3 * 1024;
+        // B fragments of the final-normed rows, once per token tile, read by every head block.
+        for (int i0 = 0; i0 < n; i0 += FTOK)
+            frag_build(xh, h, i0, std::min(FTOK, n - i0), h, fnorm_.as<float>(), c.eps, head_frags_.as<uint8_t>() + size_t(i0 / FTOK) * fb, s);
         for (size_t ci = 0; ci < prov_->n_head_chunks(); ci++) {
             HeadChunk hc = prov_->head_chunk(ci);
-            const int rows_pad = hc.mat.n_strips * STRIP;
-            if (S == 1 && hc.first == 0 && size_t(rows_pad) == vpad_) {
-                mv(hc.mat, hf_.as<float>(), h, n, logits, 1);
-            } else {
-                mv(hc.mat, hf_.as<float>(), h, n, part, S);
-                reduce_store(part, S, n, int(hc.rows), rows_pad, nullptr, logits + hc.first, int(vpad_), s);
+            for (int i0 = 0; i0 < n; i0 += FTOK) {
+                const int nt = std::min(FTOK, n - i0);
+                const size_t toff = size_t(i0 / FTOK) * tile_stride;
+                FusedArgs a;
+                a.W = hc.mat;
+                a.x = xh;
+                a.ldx = h;
+                a.norm = fnorm_.as<float>();
+                a.eps = c.eps;
+                a.frags = head_frags_.as<uint8_t>() + size_t(i0 / FTOK) * fb;
+                a.i0 = i0;
+                a.nt = nt;
+                a.out = want_logits ? logits + hc.first : nullptr;
+                a.ldo = int(vpad_);
+                a.arg_val = hpv_.as<float>() + toff + (hc.first / 256) * FTOK;
+                a.arg_idx = hpi_.as<int>() + toff + (hc.first / 256) * FTOK;
+                a.row_base = int(hc.first);
+                a.row0 = hc.first == 0 ? hpv_.as<float>() + toff + size_t(head_blocks_) * FTOK : nullptr;
+                prof_begin();
+                fused_head(a, s);
+                prof_end(hc.mat, nt);
             }
             prov_->release_head_chunk(ci);
         }
-        argmax_rows(logits, int(vpad_), int(c.vocab), n, pval_.as<float>(), pidx_.as<int>(), amax_.as<uint32_t>(), s);
+        for (int i0 = 0; i0 < n; i0 += FTOK) {
+            const int nt = std::min(FTOK, n - i0);
+            const size_t toff = size_t(i0 / FTOK) * tile_stride;
+            head_argmax_final(hpv_.as<float>() + toff, hpi_.as<int>() + toff, head_blocks_,
+                              hpv_.as<float>() + toff + size_t(head_blocks_) * FTOK, i0, nt, amax_.as<uint32_t>(), s);
+        }
     }
     prov_->end_forward();
     pos_ += t;
-}
-
-// Copy a call's tokens to the device once. The pinned staging buffer holds max_ctx tokens and
-// is only rewritten by the next call, after this call has drained the stream.
-const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
-    std::memcpy(h_tok_.p, tok, n * 4);
-    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
-    return tok_.as<uint32_t>();
 }
 
 void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax) {
@@ -627,8 +692,10 @@ void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argm
     const size_t n_chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
     for (size_t ci = 0; ci < n_chunks; ci++) {
         const size_t a = ci * PREFILL_CHUNK, len = std::min(PREFILL_CHUNK, n - a);
-        forward_chunk(tok + a, dtok + a, len, ci + 1 == n_chunks ? 1 : 0);
+        chunk_index_ = ci;
+        forward_chunk(tok + a, dtok + a, len, ci + 1 == n_chunks ? 1 : 0, logits != nullptr);
     }
+    chunk_index_ = 0;
     if (logits) HIPC(hipMemcpyAsync(logits, logits_.p, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
     if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
@@ -642,7 +709,8 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
     if (n_logits == 0 || n_logits > n)
         fail("asked for logits at " + std::to_string(n_logits) + " positions of " + std::to_string(n) + " tokens");
     if (n > PREFILL_CHUNK) fail("forward_multi takes at most 128 tokens at a time");
-    forward_chunk(tok, stage_tokens(tok, n), n, n_logits);
+    chunk_index_ = 0;
+    forward_chunk(tok, stage_tokens(tok, n), n, n_logits, logits != nullptr);
     if (logits)
         HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.p, vpad_ * 4, cfg_.vocab * 4, n_logits, hipMemcpyDeviceToHost,
                               stream_));
@@ -657,9 +725,10 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     check_request(block, n);
     if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
     const size_t p = pos_;
+    chunk_index_ = 0;
     HIPC(hipEventRecord(ev0_, stream_));
     const uint32_t* dtok = stage_tokens(block, n);
-    forward_chunk(block, dtok, n, n);
+    forward_chunk(block, dtok, n, n, false);
     accept_greedy(amax_.as<uint32_t>(), dtok, int(n), acc_.as<uint32_t>(), stream_);
     HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
     HIPC(hipEventRecord(ev1_, stream_));

@@ -7,6 +7,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "fused.hpp"
 #include "kernels.hpp"
 #include "source.hpp"
 
@@ -43,29 +44,30 @@ struct PinnedBuf {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
-// One transformer layer on the device: q/k/v fused into one matrix (rows h, kv, kv), gate and
-// up fused (rows inter, inter), plus f32 bias and norm vectors.
+// One transformer layer on the device, tile layout: q|k|v fused (rows h, kv, kv), gate|up fused
+// with 64-row blocks interleaved (gate block a, up block a, ...), o and down; f32 bias and norms.
 struct DevLayer {
-    DevMat qkv, o, gu, down;
+    TMat qkv, o, gu, down;
     const float* b_qkv = nullptr;
     const float* in_norm = nullptr;
     const float* post_norm = nullptr;
 };
 
-// Byte offsets of one layer (or one head chunk) inside a device arena.
+// Byte offsets of one layer inside a device arena.
 struct LayerArena {
+    TMat qkv, o, gu, down;  // shapes
     size_t qkv_d, qkv_s, o_d, o_s, gu_d, gu_s, down_d, down_s, b_qkv, in_norm, post_norm, total;
 };
 LayerArena layer_arena(const Config& c);
-DevLayer bind_layer(const Config& c, const LayerArena& a, uint8_t* base);
-DevMat bind_mat(uint8_t* data, uint16_t* scales, const Format& f, int rows, int cols);
-// Convert a raw layer block (reference layout, already on the device) into the arena.
+DevLayer bind_layer(const LayerArena& a, uint8_t* base);
+void clear_layer(const LayerArena& a, uint8_t* base, hipStream_t s);
+// Rearrange a raw layer block (reference layout, already on the device) into the arena.
 void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* raw_dev, const LayerArena& a, uint8_t* base,
                         hipStream_t s);
 
 struct HeadChunk {
     size_t first = 0, rows = 0;
-    DevMat mat;
+    TMat mat;
 };
 
 constexpr size_t HEAD_ROWS = 4096;  // src/provider.rs:21
@@ -84,7 +86,6 @@ public:
     // x[t][h] = embedding rows of host tokens (device tokens copy for the resident table).
     virtual void embed(const uint32_t* host_tokens, const uint32_t* dev_tokens, int t, float* x) = 0;
     virtual ls_report report() const = 0;
-    int head_splits = 1;  // K split of the output head, the same in every mode
 };
 
 std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t compute);
@@ -111,22 +112,27 @@ public:
 
 private:
     void check_request(const uint32_t* tok, size_t n) const;
-    void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits);
+    // Pushes t tokens through every layer; with n_logits > 0 also the head for the last rows,
+    // logits stored when want_logits.
+    void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits);
     const uint32_t* stage_tokens(const uint32_t* tok, size_t n);
-    // A weight-streaming matvec, bracketed by profiling events when enabled.
-    void mv(const DevMat& W, const float* x, int ldx, int t, float* part, int splits);
+    // B fragments of rows [i0, i0+nt) of x in global memory when they do not fit in LDS
+    // (nullptr: the kernel builds them in LDS).
+    const uint8_t* global_frags(const float* x, int i0, int nt, int cols, const float* w);
     void harvest();
+    void prof_begin();
+    void prof_end(const TMat& W, int nt);
 
     Config cfg_;
     int device_;
-    size_t max_ctx_, pos_ = 0;
+    size_t max_ctx_, pos_ = 0, chunk_index_ = 0;
     hipStream_t stream_ = nullptr;
     std::unique_ptr<DeviceProvider> prov_;
-    DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_;
-    DevBuf x_, xn_, qkv_, attn_, gu_, act_, part_, scores_, logits_, hf_, amax_, pval_, pidx_, tok_, acc_;
-    PinnedBuf h_tok_, h_out_;
-    size_t part_floats_ = 0, vpad_ = 0;
-    int s_qkv_ = 1, s_o_ = 1, s_gu_ = 1, s_down_ = 1;
+    DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_, pos_dev_;
+    DevBuf x_, q_, attn_, act_frags_, in_frags_, head_frags_, attn_scratch_, logits_, hpv_, hpi_, amax_, tok_, acc_;
+    PinnedBuf h_tok_, h_out_, h_pos_;
+    size_t vpad_ = 0, act_frag_bytes_ = 0;
+    int head_blocks_ = 0;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     bool prof_ = false;
