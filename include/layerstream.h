@@ -172,6 +172,13 @@ typedef struct {
 int ls_model_profile(ls_model* m, int enable);
 int ls_model_profile_read(ls_model* m, ls_kernel_stat* out);
 
+/* Graph replay of the verify step (no counterpart in the reference, whose forward pass is a
+ * CPU loop): with enable != 0 (the default) a resident model captures ls_model_verify_greedy
+ * for each block length once into a HIP graph and replays it, so a step costs one launch on
+ * the host. Results are bit-identical either way; profiling and streamed weights always run
+ * the step launch by launch. */
+int ls_model_use_graphs(ls_model* m, int enable);
+
 /* ---------------------------------------------------------------------------------------
  * Speculative decoding: speculative_greedy (src/spec.rs:57-152).
  * ------------------------------------------------------------------------------------- */

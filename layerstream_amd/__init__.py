@@ -143,6 +143,7 @@ SIGNATURES = {
     "ls_spec_free": (None, [P]),
     "ls_model_profile": (C.c_int, [P, C.c_int]),
     "ls_model_profile_read": (C.c_int, [P, C.POINTER(KernelStat)]),
+    "ls_model_use_graphs": (C.c_int, [P, C.c_int]),
     "ls_matmul": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
 }
 
@@ -409,6 +410,10 @@ class Model:
         st = KernelStat()
         _check(lib().ls_model_profile_read(self.h, C.byref(st)))
         return {f: getattr(st, f) for f, _ in KernelStat._fields_}
+
+    def use_graphs(self, enable: bool):
+        """Replay verify steps from captured HIP graphs (default on; resident weights only)."""
+        _check(lib().ls_model_use_graphs(self.h, int(enable)))
 
 
 class ModelDrafter:

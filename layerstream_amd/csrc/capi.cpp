@@ -357,6 +357,13 @@ int ls_model_profile(ls_model* m, int enable) {
     });
 }
 
+int ls_model_use_graphs(ls_model* m, int enable) {
+    return guard([&] {
+        need(m, "model");
+        m->m->set_graphs(enable != 0);
+    });
+}
+
 int ls_model_profile_read(ls_model* m, ls_kernel_stat* out) {
     return guard([&] {
         need(m, "model");
@@ -395,24 +402,23 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
         ls::tile_clear(W, s);
         ls::tile_repack(static_cast<const uint8_t*>(w_dev), int(rows), W, 0, int(rows), int(rows), s);
         HIPC(hipMemsetAsync(y_dev, 0, t * rows * 4, s));
-        const size_t fb = size_t(ls::tile_kpad(int(cols))) / 32 * 3 * 1024;
-        ls::DevBuf frags(fb > 96 * 1024 ? fb : 0);
-        for (int i0 = 0; i0 < int(t); i0 += ls::FTOK) {
-            const int nt = std::min(ls::FTOK, int(t) - i0);
-            ls::FusedArgs a;
-            a.W = W;
-            a.x = x_dev;
-            a.ldx = int(cols);
-            a.i0 = i0;
-            a.nt = nt;
-            a.out = y_dev;
-            a.ldo = int(rows);
-            if (frags.p) {
-                ls::frag_build(x_dev, int(cols), i0, nt, int(cols), nullptr, 0.0f, frags.as<uint8_t>(), s);
-                a.frags = frags.as<uint8_t>();
-            }
-            ls::fused_residual(a, 16, s);
-        }
+        // y = W x through the residual kernel (y starts at zero), inputs as fragments.
+        const size_t tiles = (t + ls::FTOK - 1) / ls::FTOK;
+        ls::DevBuf frags(ls::frag_tile_bytes(int(cols)) * tiles);
+        HIPC(hipMemsetAsync(frags.p, 0, frags.n, s));
+        ls::x_frags(x_dev, int(t), int(cols), nullptr, frags.as<uint8_t>(), nullptr, s);
+        const ls::MMPlan plan = ls::mm_plan(W, 1, 8, int(t));
+        ls::DevBuf part(std::max<size_t>(1, ls::mm_part_floats(plan)) * 4);
+        ls::DevBuf cnt(std::max<size_t>(1, ls::mm_counters(plan)) * 4);
+        HIPC(hipMemsetAsync(cnt.p, 0, cnt.n, s));
+        ls::MMArgs a;
+        a.W = W;
+        a.frags = frags.as<uint8_t>();
+        a.frag_stride = ls::frag_tile_bytes(int(cols));
+        a.n = int(t);
+        a.out = y_dev;
+        a.ldo = int(rows);
+        ls::mm_residual(a, plan, ls::MMScratch{part.as<float>(), cnt.as<int>()}, s);
         HIPC(hipStreamSynchronize(s));
     });
 }

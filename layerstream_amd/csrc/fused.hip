@@ -1,15 +1,19 @@
 // Fused MFMA kernels of the verify step for gfx950 (CDNA4, wave64, v_mfma_f32_16x16x32_bf16).
 //
-// One launch handles one tile of up to 16 tokens. A workgroup owns 64 * RG weight rows and splits
-// the padded K range into KSPLIT contiguous pieces, one wavefront each; a wavefront streams four
-// 16-row strips of its piece, one 1 KiB load per strip and chunk, converts the int8 / int4 / bf16
-// weights to bf16 in registers and issues three MFMAs per strip and k-step (one per input term).
-// Group scales multiply each group's accumulator. The pieces are summed in a fixed order in LDS and
-// an epilogue consumes the [rows][tokens] tile. Every output element's arithmetic depends only on
-// the matrix shape, never on the number of tokens in the launch: a verify pass over k+1 tokens
-// gives the same bits as k+1 single-token passes (src/spec.rs:8-11).
+// A launch covers every 16-token tile of its tokens (grid.y). A workgroup owns rg groups of 64
+// weight rows and one K range; each of its wavefronts streams four 16-row strips over 128 columns
+// of that range (4 k-steps), issuing every weight and input-fragment load of its share at once,
+// then converts the int8 / int4 / bf16 weights to bf16 in registers and issues three MFMAs per
+// strip and k-step (one per input term). Group scales multiply each group's accumulator. The
+// wavefronts of a row group are summed in a fixed order in LDS; when the K range is split over
+// several workgroups, each stores its piece and the last one of the row block to arrive (an
+// atomic counter) adds the pieces in split order and runs the epilogue. Every output element's
+// arithmetic depends only on the matrix shape, never on the number of tokens in the launch: a
+// verify pass over k+1 tokens gives the same bits as k+1 single-token passes (src/spec.rs:8-11).
 #include "fused.hpp"
+#include "frag_dev.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <stdexcept>
 #include <string>
@@ -24,6 +28,7 @@ namespace ls {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------------
 // Layout
@@ -112,10 +117,54 @@ void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int
     FCHECK(hipGetLastError());
 }
 
-__global__ void k_tile_embed(TMat E, const uint32_t* __restrict__ tokens, float* __restrict__ x) {
+// Sum of squares of 64 values v(0..63) in the one order used everywhere: eight sequential sums
+// of eight, added in order.
+template <class F>
+__device__ __forceinline__ float ss64(F v, int n) {
+    float s = 0.0f;
+    for (int b = 0; b < 8; b++) {
+        float sb = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int c = 8 * b + j;
+            const float x = c < n ? v(c) : 0.0f;
+            sb = __builtin_fmaf(x, x, sb);
+        }
+        s += sb;
+    }
+    return s;
+}
+
+// Row i of x -> fragment slots of token i (x * w when w is set) and per-64-column sums of
+// squares. The row (cols values, a multiple of 8) is staged in LDS; one workgroup per token.
+__device__ void row_frags(const float* xr, int i, int cols, const float* __restrict__ w, uint8_t* frags, float* ss,
+                          float* lds) {
+    if (xr != lds)
+        for (int c = threadIdx.x; c < cols; c += blockDim.x) lds[c] = xr[c];
+    __syncthreads();
+    const int tile = i / FTOK, tok = i % FTOK;
+    uint8_t* tf = frags + size_t(tile) * frag_tile_bytes(cols);
+    for (int sl = threadIdx.x; sl < cols / 8; sl += blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = w ? __fmul_rn(lds[8 * sl + j], w[8 * sl + j]) : lds[8 * sl + j];
+        write_slot(tf, sl / 4, tok + 16 * (sl % 4), v);
+    }
+    if (!ss) return;
+    const int slots = ss_slots(cols);
+    for (int g = threadIdx.x; g < slots; g += blockDim.x) {
+        const int n = min(64, cols - 64 * g);
+        ss[(size_t(tile) * slots + g) * FTOK + tok] = ss64([&](int c) { return lds[64 * g + c]; }, n);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_tile_embed(TMat E, const uint32_t* __restrict__ tokens, float* __restrict__ x,
+                                                    const float* __restrict__ w, uint8_t* frags, float* ss) {
+    extern __shared__ float lds[];
     const int i = blockIdx.x;
     const int r = int(tokens[i]), strip = r / 16, rl = r % 16;
     const int cc = tile_chunk_cols(E.bits);
+    float* xr = x + size_t(i) * E.cols;
     for (int col = threadIdx.x; col < E.cols; col += blockDim.x) {
         const int c = col / cc, q = (col % cc) / 32, lg = (col % 32) / 8, j = col % 8;
         const uint8_t* slot = E.data + ((size_t(strip) * E.n_chunks + c) * 64 + rl + 16 * lg) * 16;
@@ -133,84 +182,28 @@ __global__ void k_tile_embed(TMat E, const uint32_t* __restrict__ tokens, float*
             const uint16_t sb = E.scales[(size_t(strip) * E.n_groups + col / E.group) * 16 + rl];
             v = qv * __uint_as_float(uint32_t(sb) << 16);
         }
-        x[size_t(i) * E.cols + col] = v;
+        xr[col] = v;
+        lds[col] = v;
     }
+    if (frags) row_frags(lds, i, E.cols, w, frags, ss, lds);
 }
 
-void tile_embed(const TMat& E, const uint32_t* tokens, int t, float* x, hipStream_t s) {
-    hipLaunchKernelGGL(k_tile_embed, dim3(t), dim3(256), 0, s, E, tokens, x);
+void tile_embed(const TMat& E, const uint32_t* tokens, int n, float* x, const float* w, uint8_t* frags, float* ss,
+                hipStream_t s) {
+    if (E.cols % 8) throw std::runtime_error("embedding width must be a multiple of 8");
+    hipLaunchKernelGGL(k_tile_embed, dim3(n), dim3(256), size_t(E.cols) * 4, s, E, tokens, x, w, frags, ss);
     FCHECK(hipGetLastError());
 }
 
-// ---------------------------------------------------------------------------------------
-// B fragments: f32 value -> three bf16 terms (truncations) whose sum is the value exactly.
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void split3(float v, uint32_t& h, uint32_t& m, uint32_t& l) {
-    const uint32_t vb = __float_as_uint(v);
-    const float hv = __uint_as_float(vb & 0xffff0000u);
-    const float r1 = v - hv;
-    const uint32_t r1b = __float_as_uint(r1);
-    const float mv = __uint_as_float(r1b & 0xffff0000u);
-    const float r2 = r1 - mv;
-    h = vb >> 16;
-    m = r1b >> 16;
-    l = __float_as_uint(r2) >> 16;
+__global__ __launch_bounds__(256) void k_x_frags(const float* __restrict__ x, int cols, const float* __restrict__ w,
+                                                 uint8_t* frags, float* ss) {
+    extern __shared__ float lds[];
+    row_frags(x + size_t(blockIdx.x) * cols, blockIdx.x, cols, w, frags, ss, lds);
 }
 
-// Fragment slot p = (k-step, lane): token lane % 16, columns 32 ks + 8 (lane / 16) + j.
-__device__ __forceinline__ void build_frag_slot(int p, const float* __restrict__ x, int ldx, int i0, int nt, int K,
-                                                const float* __restrict__ w, const float* inv, uint8_t* dst) {
-    const int ks = p >> 6, lane = p & 63, tok = lane & 15;
-    const int col0 = 32 * ks + 8 * (lane >> 4);
-    uint32_t H[4], M[4], L[4];
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        float v0 = 0.0f, v1 = 0.0f;
-        if (tok < nt) {
-            const float* xr = x + size_t(i0 + tok) * ldx;
-            const float iv = inv ? inv[tok] : 1.0f;
-            if (col0 + j < K) v0 = w ? __fmul_rn(__fmul_rn(xr[col0 + j], iv), w[col0 + j]) : xr[col0 + j];
-            if (col0 + j + 1 < K) v1 = w ? __fmul_rn(__fmul_rn(xr[col0 + j + 1], iv), w[col0 + j + 1]) : xr[col0 + j + 1];
-        }
-        uint32_t h0, m0, l0, h1, m1, l1;
-        split3(v0, h0, m0, l0);
-        split3(v1, h1, m1, l1);
-        H[j / 2] = h0 | (h1 << 16);
-        M[j / 2] = m0 | (m1 << 16);
-        L[j / 2] = l0 | (l1 << 16);
-    }
-    uint4* o = reinterpret_cast<uint4*>(dst + (size_t(ks) * 3 * 64 + lane) * 16);
-    o[0] = make_uint4(H[0], H[1], H[2], H[3]);
-    o[64] = make_uint4(M[0], M[1], M[2], M[3]);
-    o[128] = make_uint4(L[0], L[1], L[2], L[3]);
-}
-
-// Per-token 1 / sqrt(mean(x^2) + eps) (src/kernels.rs:217-228): token i is always reduced by one
-// wavefront with lane-strided partial sums and a fixed shuffle tree.
-__device__ void norm_invs(const float* __restrict__ x, int ldx, int i0, int nt, int K, float eps, float* inv, int nwaves) {
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int tok = wv; tok < nt; tok += nwaves) {
-        const float* xr = x + size_t(i0 + tok) * ldx;
-        float ss = 0.0f;
-        for (int c = lane; c < K; c += 64) ss = __builtin_fmaf(xr[c], xr[c], ss);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        if (lane == 0) inv[tok] = 1.0f / sqrtf(ss / float(K) + eps);
-    }
-}
-
-__global__ __launch_bounds__(256) void k_frag_build(const float* __restrict__ x, int ldx, int i0, int nt, int K,
-                                                    const float* __restrict__ w, float eps, uint8_t* __restrict__ frags) {
-    __shared__ float inv[FTOK];
-    if (w) norm_invs(x, ldx, i0, nt, K, eps, inv, 4);
-    __syncthreads();
-    const int n = tile_kpad(K) / 32 * 64;
-    for (int p = blockIdx.x * 256 + threadIdx.x; p < n; p += gridDim.x * 256) build_frag_slot(p, x, ldx, i0, nt, K, w, w ? inv : nullptr, frags);
-}
-
-void frag_build(const float* x, int ldx, int i0, int nt, int cols, const float* w, float eps, uint8_t* frags, hipStream_t s) {
-    const int n = tile_kpad(cols) / 32 * 64;
-    hipLaunchKernelGGL(k_frag_build, dim3((n + 255) / 256), dim3(256), 0, s, x, ldx, i0, nt, cols, w, eps, frags);
+void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, float* ss, hipStream_t s) {
+    if (cols % 8) throw std::runtime_error("row width must be a multiple of 8");
+    hipLaunchKernelGGL(k_x_frags, dim3(n), dim3(256), size_t(cols) * 4, s, x, cols, w, frags, ss);
     FCHECK(hipGetLastError());
 }
 
@@ -259,16 +252,12 @@ __device__ __forceinline__ f32x4 scales4(const uint16_t* __restrict__ sc, int st
                  __uint_as_float(v.y & 0xffff0000u)};
 }
 
-// A wavefront's share of the matrix: four strips s0..s0+3 over chunks [c0, c1). Weight loads
-// run PF chunks ahead of the MFMAs: the first PF chunks are requested before the caller's
-// prologue, so HBM latency overlaps the input normalisation.
-constexpr int PF = 2;
-
-struct WaveLoads {
-    uint4 buf[PF][4];
+// Chunks per wavefront: every wavefront covers 4 k-steps (128 columns).
+template <int BITS>
+struct Steps {
+    static constexpr int Q = BITS == 16 ? 1 : (BITS == 8 ? 2 : 4);  // k-steps per chunk
+    static constexpr int CPW = 4 / Q;                                // chunks per wavefront
 };
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Weights are read once per pass: non-temporal loads keep them from displacing the activations.
 __device__ __forceinline__ void load_chunk(const uint8_t* base, size_t sstride, int c, uint4* raw) {
@@ -279,37 +268,25 @@ __device__ __forceinline__ void load_chunk(const uint8_t* base, size_t sstride, 
     }
 }
 
-__device__ __forceinline__ void wave_prefetch(const TMat& W, int s0, int c0, int c1, WaveLoads& L) {
-    const int lane = threadIdx.x & 63;
-    const uint8_t* base = W.data + (size_t(s0) * W.n_chunks * 64 + lane) * 16;
-    const size_t sstride = size_t(W.n_chunks) * 64 * 16;
-#pragma unroll
-    for (int p = 0; p < PF; p++)
-        if (c0 + p < c1) load_chunk(base, sstride, c0 + p, L.buf[p]);
-}
-
-// One chunk: Q k-steps x 4 strips x 3 MFMAs, with group scaling.
+// One chunk: Q k-steps x 4 strips x 3 MFMAs, with group scaling. B[q][term] are the fragments of
+// the chunk's k-steps; [ks_begin, ks_end) is the wavefront's k-step range.
 template <int BITS, bool G16>
-__device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_begin, int ks_end, const uint4* fr,
+__device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_begin, int ks_end, const uint4 (*B)[3],
                                            const uint4* raw, f32x4* acc, f32x4* total) {
     const int lane = threadIdx.x & 63;
-    constexpr int Q = BITS == 16 ? 1 : (BITS == 8 ? 2 : 4);
+    constexpr int Q = Steps<BITS>::Q;
     const int G = W.group;
-#pragma unroll(BITS == 4 ? 1 : Q)
+#pragma unroll
     for (int q = 0; q < Q; q++) {
         const int ks = c * Q + q;
-        uint4 B[3];
-        B[0] = fr[(ks * 3 + 0) * 64 + lane];
-        B[1] = fr[(ks * 3 + 1) * 64 + lane];
-        B[2] = fr[(ks * 3 + 2) * 64 + lane];
         if constexpr (BITS == 16) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) total[r] = mfma3(a_operand<BITS>(raw[r], q), B, total[r]);
+            for (int r = 0; r < 4; r++) total[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], total[r]);
         } else if constexpr (!G16) {
             const bool first = (ks * 32) % G == 0 || ks == ks_begin;
             const bool last = ((ks + 1) * 32) % G == 0 || ks == ks_end - 1;
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = mfma3(a_operand<BITS>(raw[r], q), B, first ? f32x4{0, 0, 0, 0} : acc[r]);
+            for (int r = 0; r < 4; r++) acc[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], first ? f32x4{0, 0, 0, 0} : acc[r]);
             if (last) {
                 const int g = ks * 32 / G;
 #pragma unroll
@@ -325,8 +302,8 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint4 A = a_operand<BITS>(raw[r], q), Z = make_uint4(0, 0, 0, 0);
-                const f32x4 a1 = mfma3(lo ? A : Z, B, f32x4{0, 0, 0, 0});
-                const f32x4 a2 = mfma3(lo ? Z : A, B, f32x4{0, 0, 0, 0});
+                const f32x4 a1 = mfma3(lo ? A : Z, B[q], f32x4{0, 0, 0, 0});
+                const f32x4 a2 = mfma3(lo ? Z : A, B[q], f32x4{0, 0, 0, 0});
                 const f32x4 s1 = scales4(W.scales, s0 + r, W.n_groups, 2 * ks, lane);
                 const f32x4 s2 = scales4(W.scales, s0 + r, W.n_groups, 2 * ks + 1, lane);
 #pragma unroll
@@ -339,183 +316,297 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
     }
 }
 
-template <int BITS, bool G16>
-__device__ __forceinline__ void wave_tiles(const TMat& W, int s0, int c0, int c1, const uint4* fr, WaveLoads& L, f32x4* total) {
-    const int lane = threadIdx.x & 63;
-    constexpr int Q = BITS == 16 ? 1 : (BITS == 8 ? 2 : 4);
-    const int ks_begin = c0 * Q, ks_end = c1 * Q;
-    const uint8_t* base = W.data + (size_t(s0) * W.n_chunks * 64 + lane) * 16;
-    const size_t sstride = size_t(W.n_chunks) * 64 * 16;
-    f32x4 acc[4];
+enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_HEAD = 3 };
+
+// 1 / rms per token of a tile from the producer's sum-of-squares partials, by one wavefront:
+// lane (part, token) adds slots part, part + 4, ... in order (every load issued first), then a
+// fixed shuffle tree over the four parts (src/kernels.rs:217-228 up to the summation order).
+constexpr int SS_SLOTS_MAX = 64;
+__device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, float* inv) {
+    const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
+    const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
+    float x[SS_SLOTS_MAX / 4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
-    for (int c = c0; c < c1; c += PF) {
+    for (int k = 0; k < SS_SLOTS_MAX / 4; k++) {
+        const int sl = part + 4 * k;
+        x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
+    }
+    float v = 0.0f;
 #pragma unroll
-        for (int p = 0; p < PF; p++) {
-            if (c + p < c1) {
-                chunk_mfma<BITS, G16>(W, s0, c + p, ks_begin, ks_end, fr, L.buf[p], acc, total);
-                if (c + p + PF < c1) load_chunk(base, sstride, c + p + PF, L.buf[p]);
+    for (int k = 0; k < SS_SLOTS_MAX / 4; k++) v += x[k];
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (lane < FTOK) inv[lane] = 1.0f / sqrtf(v / float(cols) + a.eps);
+}
+
+__device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
+    const bool an = isnan(va), bn = isnan(vb);
+    if (an != bn) return !an;
+    if (an) return ia < ib;
+    if (va != vb) return va > vb;
+    return ia < ib;
+}
+
+// Cache policy of the split-K pieces: sc1, coherent across the L2s of the XCDs.
+constexpr int CPOL_SC1 = 16;
+constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
+constexpr int MAX_SPLIT = 16;
+constexpr int ROPE_HALF_MAX = 128;
+
+// Dynamic LDS: [wavefront sums (kw > 1)] [tile: 64 rg rows x 16 floats] [16 inverse rms]
+// [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
+// 64 rg x 16, per-row vector 64 rg, RoPE cos and sin 2 x 16 x half].
+template <int BITS, int EPI, bool G16>
+__global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+    constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nw = p.rg * p.kw, nthr = nw * 64;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int tile = blockIdx.y, rb = blockIdx.x / p.nsplit, sp = blockIdx.x % p.nsplit;
+    const int rows_wg = 64 * p.rg, row0 = rb * rows_wg;
+    const int nt = min(FTOK, a.n - tile * FTOK);
+    const TMat& W = a.W;
+    const int rgi = wv / p.kw, kw = wv % p.kw;
+    const int s0 = (rb * p.rg + rgi) * 4;
+    const int c0 = (sp * p.kw + kw) * CPW;
+    const int nch = min(CPW, W.n_chunks - c0);  // chunks of this wavefront (none when <= 0)
+
+    const size_t red_bytes = p.kw > 1 ? size_t(nw) * 4 * 64 * 16 : 0;
+    float* tl = reinterpret_cast<float*>(smem + red_bytes);
+    float* inv = tl + rows_wg * FTOK;
+    int* flag = reinterpret_cast<int*>(inv + FTOK);
+    float* bv = reinterpret_cast<float*>(flag + 4);
+    int* bi = reinterpret_cast<int*>(bv + FTOK * 16);
+    float* xs = reinterpret_cast<float*>(bi + FTOK * 16);
+    float* vec = xs + rows_wg * FTOK;
+    float* rcos = vec + rows_wg;
+    float* rsin = rcos + FTOK * ROPE_HALF_MAX;
+    const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
+
+    // Every load of the wavefront's share is issued before any arithmetic.
+    uint4 raw[CPW][4];
+    uint4 B[CPW * Q][3];
+    {
+        const uint8_t* wb = W.data + (size_t(s0) * W.n_chunks * 64 + lane) * 16;
+        const size_t sst = size_t(W.n_chunks) * 1024;
+        const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride) + lane;
+#pragma unroll
+        for (int c = 0; c < CPW; c++) {
+            if (c < nch) {
+                load_chunk(wb, sst, c0 + c, raw[c]);
+#pragma unroll
+                for (int q = 0; q < Q; q++) {
+                    const int ks = (c0 + c) * Q + q;
+#pragma unroll
+                    for (int t = 0; t < 3; t++) B[c * Q + q][t] = fb[(ks * 3 + t) * 64];
+                }
             }
         }
     }
-}
-
-enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_HEAD = 3 };
-
-struct FusedCfg {
-    int rg;          // 64-row groups per workgroup
-    int ksplit;      // wavefronts per row group
-    int frag_lds;    // 1: build B fragments in LDS from x (prologue); 0: read a.frags from global
-    int frag_bytes;  // LDS bytes of the fragments
-};
-
-// Dynamic LDS: [fragments | reduction] then [tile: rows x 16 floats] then [16 inverse norms].
-template <int BITS, int EPI, bool G16>
-__global__ __launch_bounds__(1024) void k_fused(FusedArgs a, FusedCfg cfg) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int nw = cfg.rg * cfg.ksplit;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int rows_wg = 64 * cfg.rg;
-    const size_t red_bytes = size_t(nw) * 4 * 64 * 16;
-    const size_t region = cfg.frag_bytes > int(red_bytes) ? size_t(cfg.frag_bytes) : red_bytes;
-    float* tile = reinterpret_cast<float*>(smem + region);
-    float* inv = tile + rows_wg * FTOK;
-    const TMat& W = a.W;
-
-    // This wavefront's rows and k range; its first weight chunks are requested right away.
-    const int rgi = wv / cfg.ksplit, kp = wv % cfg.ksplit;
-    const int s0 = (blockIdx.x * cfg.rg + rgi) * 4;
-    const int c0 = kp * W.n_chunks / cfg.ksplit, c1 = (kp + 1) * W.n_chunks / cfg.ksplit;
-    WaveLoads loads;
-    wave_prefetch(W, s0, c0, c1, loads);
-
-    // Prologue: B fragments of the token tile.
-    const uint4* fr;
-    if (cfg.frag_lds) {
-        if (a.norm) norm_invs(a.x, a.ldx, a.i0, a.nt, W.cols, a.eps, inv, nw);
-        __syncthreads();
-        const int n = W.n_chunks * tile_chunk_cols(BITS) / 32 * 64;
-        for (int p = threadIdx.x; p < n; p += nw * 64)
-            build_frag_slot(p, a.x, a.ldx, a.i0, a.nt, W.cols, a.norm, a.norm ? inv : nullptr, smem);
-        __syncthreads();
-        fr = reinterpret_cast<const uint4*>(smem);
-    } else {
-        fr = reinterpret_cast<const uint4*>(a.frags);
-    }
-
-    f32x4 total[4];
-    wave_tiles<BITS, G16>(W, s0, c0, c1, fr, loads, total);
-
-    // Fixed-order sum of the pieces: red[wave][strip][lane] (float4), then the tile.
-    __syncthreads();
-    f32x4* red = reinterpret_cast<f32x4*>(smem);
+    // Epilogue operands, staged in LDS while the weights are in flight.
+    if constexpr (EPI == EPI_RESID) {
+        for (int e0 = threadIdx.x; e0 < rows_wg * FTOK; e0 += 4 * nthr) {
+            float xv[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) red[(wv * 4 + r) * 64 + lane] = total[r];
-    __syncthreads();
-    for (int e = threadIdx.x; e < cfg.rg * 4 * 64; e += nw * 64) {
-        const int rg = e / 256, r = (e / 64) % 4, ln = e % 64;
-        f32x4 sum = red[((rg * cfg.ksplit) * 4 + r) * 64 + ln];
-        for (int k = 1; k < cfg.ksplit; k++) {
-            const f32x4 v = red[(((rg * cfg.ksplit) + k) * 4 + r) * 64 + ln];
+            for (int u = 0; u < 4; u++) {
+                const int e = e0 + u * nthr, rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+                xv[u] = (e < rows_wg * FTOK && tok < nt && row < W.rows) ? a.out[size_t(ibase + tok) * a.ldo + row] : 0.0f;
+            }
 #pragma unroll
-            for (int i = 0; i < 4; i++) sum[i] += v[i];
+            for (int u = 0; u < 4; u++)
+                if (e0 + u * nthr < rows_wg * FTOK) xs[e0 + u * nthr] = xv[u];
         }
+        if (a.onorm)
+            for (int r = threadIdx.x; r < rows_wg; r += nthr) vec[r] = row0 + r < W.rows ? a.onorm[row0 + r] : 0.0f;
+    } else if constexpr (EPI == EPI_QKV) {
+        for (int r = threadIdx.x; r < rows_wg; r += nthr) vec[r] = row0 + r < W.rows ? a.bias[row0 + r] : 0.0f;
+        const int half = a.hd / 2, pos0 = *a.pos0;
+        for (int e = threadIdx.x; e < nt * half; e += nthr) {
+            const int tok = e / half, j = e % half;
+            const size_t at = size_t(pos0 + ibase + tok) * half + j;
+            rcos[tok * half + j] = a.rope_cos[at];
+            rsin[tok * half + j] = a.rope_sin[at];
+        }
+    }
+    // 1 / rms per token from the producer's sum-of-squares partials (fixed order).
+    if (a.ss && wv == 0) inv_rms(a, tile, W.cols, inv);
+
+    f32x4 total[4], acc[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) tile[(64 * rg + 16 * r + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
+    for (int r = 0; r < 4; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < CPW; c++)
+        if (c < nch) chunk_mfma<BITS, G16>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
+
+    // Row-group tile: the kw wavefront sums added in wavefront order.
+    if (p.kw > 1) {
+        f32x4* red = reinterpret_cast<f32x4*>(smem);
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[(wv * 4 + r) * 64 + lane] = total[r];
+        __syncthreads();
+        for (int e = threadIdx.x; e < p.rg * 256; e += nthr) {
+            const int g = e >> 8, r = (e >> 6) & 3, ln = e & 63;
+            f32x4 sum = red[((g * p.kw) * 4 + r) * 64 + ln];
+            for (int k = 1; k < p.kw; k++) {
+                const f32x4 v = red[((g * p.kw + k) * 4 + r) * 64 + ln];
+#pragma unroll
+                for (int i = 0; i < 4; i++) sum[i] += v[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) tl[(64 * g + 16 * r + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) tl[(64 * rgi + 16 * r + 4 * (lane >> 4) + i) * FTOK + (lane & 15)] = total[r][i];
     }
     __syncthreads();
 
-    // Epilogues over tile[row_local][token].
-    const int row0 = blockIdx.x * rows_wg;
+    // Split K: store this piece; the last workgroup of the row block adds all pieces in split
+    // order. Pieces move with 128-bit sc1 buffer accesses and the counter with an agent-scope
+    // atomic, all coherent across the L2s of the XCDs; the stores are complete (s_waitcnt)
+    // before the counter moves.
+    if (p.nsplit > 1) {
+        const int elems = rows_wg * FTOK, e4n = elems / 4;
+        float* base = sc.part + (size_t(tile) * p.nrb + rb) * p.nsplit * elems;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(base, 0, p.nsplit * elems * 4, BUF_DWORD3);
+        const f32x4* tl4 = reinterpret_cast<const f32x4*>(tl);
+        for (int e4 = threadIdx.x; e4 < e4n; e4 += nthr)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, tl4[e4]), rs, (sp * elems + 4 * e4) * 4, 0, CPOL_SC1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int* cn = sc.cnt + size_t(tile) * p.nrb + rb;
+            const int old = __hip_atomic_fetch_add(cn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == p.nsplit - 1;
+            if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            flag[0] = last;
+        }
+        __syncthreads();
+        if (!flag[0]) return;
+        f32x4* tw = reinterpret_cast<f32x4*>(tl);
+        for (int e4 = threadIdx.x; e4 < e4n; e4 += nthr) {
+            f32x4 v[MAX_SPLIT];
+#pragma unroll
+            for (int k = 0; k < MAX_SPLIT; k++)
+                if (k < p.nsplit)
+                    v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (k * elems + 4 * e4) * 4, 0, CPOL_SC1));
+            f32x4 sum = v[0];
+#pragma unroll
+            for (int k = 1; k < MAX_SPLIT; k++)
+                if (k < p.nsplit)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sum[i] += v[k][i];
+            tw[e4] = sum;
+        }
+        __syncthreads();
+    }
+
     if constexpr (EPI == EPI_QKV) {
         // rows: [0, h) q heads, [h, h + kv) k heads, [h + kv, h + 2 kv) v heads
-        const int hd = a.hd, half = hd / 2, h = a.heads * hd, kv = a.kv_heads * hd;
+        const int hd = a.hd, half = hd / 2, h = a.heads * hd, kvd = a.kv_heads * hd;
         const int pos0 = *a.pos0;
-        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nw * 64) {
+        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-            if (tok >= a.nt || row >= W.rows) continue;
-            tile[rl * FTOK + tok] += a.bias[row];
+            if (tok >= nt || row >= W.rows) continue;
+            const float v = a.ss ? __fmul_rn(tl[e], inv[tok]) : tl[e];
+            tl[e] = __fadd_rn(v, vec[rl]);
         }
         __syncthreads();
-        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nw * 64) {
+        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-            if (tok >= a.nt || row >= W.rows) continue;
-            const int i = a.i0 + tok, pos = pos0 + i;
-            float v = tile[rl * FTOK + tok];
-            if (row < h + kv) {  // RoPE, rotate half (src/kernels.rs:242-252)
+            if (tok >= nt || row >= W.rows) continue;
+            const int i = ibase + tok, pos = pos0 + i;
+            float v = tl[e];
+            if (row < h + kvd) {  // RoPE, rotate half (src/kernels.rs:242-252)
                 const int d = row % hd, j = d % half;
-                const float c = a.rope_cos[size_t(pos) * half + j], sn = a.rope_sin[size_t(pos) * half + j];
+                const float c = rcos[tok * half + j], sn = rsin[tok * half + j];
                 if (d < half) {
-                    const float b = tile[(rl + half) * FTOK + tok];
+                    const float b = tl[(rl + half) * FTOK + tok];
                     v = __fsub_rn(__fmul_rn(v, c), __fmul_rn(b, sn));
                 } else {
-                    const float aa = tile[(rl - half) * FTOK + tok];
+                    const float aa = tl[(rl - half) * FTOK + tok];
                     v = __fadd_rn(__fmul_rn(v, c), __fmul_rn(aa, sn));
                 }
             }
             if (row < h) a.out[size_t(i) * a.ldo + row] = v;
-            else if (row < h + kv) a.kcache[size_t(pos) * kv + (row - h)] = v;
-            else a.vcache[size_t(pos) * kv + (row - h - kv)] = v;
+            else if (row < h + kvd) a.kcache[size_t(pos) * kvd + (row - h)] = v;
+            else a.vcache[size_t(pos) * kvd + (row - h - kvd)] = v;
         }
     } else if constexpr (EPI == EPI_RESID) {
-        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nw * 64) {
+        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-            if (tok >= a.nt || row >= W.rows) continue;
-            float* o = a.out + size_t(a.i0 + tok) * a.ldo + row;
-            *o = *o + tile[rl * FTOK + tok];
+            float xn = 0.0f;
+            if (tok < nt && row < W.rows) {
+                xn = __fadd_rn(xs[e], tl[e]);
+                a.out[size_t(ibase + tok) * a.ldo + row] = xn;
+            }
+            tl[e] = xn;
+        }
+        __syncthreads();
+        if (a.ofrags) {
+            uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
+            for (int sl = threadIdx.x; sl < (rows_wg / 32) * 64; sl += nthr) {
+                const int ksl = sl >> 6, ln = sl & 63, tok = ln & 15;
+                const int cl = 32 * ksl + 8 * (ln >> 4);
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float x = tl[(cl + j) * FTOK + tok];
+                    v[j] = a.onorm ? __fmul_rn(x, vec[cl + j]) : x;
+                }
+                write_slot(tf, row0 / 32 + ksl, ln, v);
+            }
+        }
+        if (a.oss) {
+            for (int e = threadIdx.x; e < p.rg * FTOK; e += nthr) {
+                const int g = e / FTOK, tok = e % FTOK, slot = row0 / 64 + g;
+                if (slot >= a.oss_slots) continue;
+                a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] =
+                    ss64([&](int c) { return tl[(64 * g + c) * FTOK + tok]; }, 64);
+            }
         }
     } else if constexpr (EPI == EPI_SILU) {
-        // rows: [64 gate rows | 64 up rows] for act columns 64 * blockIdx.x + [0, 64)
-        for (int p = threadIdx.x; p < 2 * 64; p += nw * 64) {
-            const int ksl = p / 64, ln = p % 64, tok = ln & 15;
-            const int colb = 32 * ksl + 8 * (ln >> 4);
-            const int col0 = 64 * blockIdx.x + colb;
-            uint32_t H[4], M[4], L[4];
+        // rows: [64 gate rows | 64 up rows] for act columns 64 * rb + [0, 64)
+        uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
+        for (int sl = threadIdx.x; sl < 2 * 64; sl += nthr) {
+            const int ksl = sl >> 6, ln = sl & 63, tok = ln & 15;
+            const int cl = 32 * ksl + 8 * (ln >> 4);
+            float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-                float v[2];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    v[u] = 0.0f;
-                    if (tok < a.nt) {
-                        const float g = tile[(colb + j + u) * FTOK + tok], up = tile[(64 + colb + j + u) * FTOK + tok];
-                        v[u] = __fmul_rn(g / (1.0f + expf(-g)), up);
+            for (int j = 0; j < 8; j++) {
+                v[j] = 0.0f;
+                if (tok < nt) {
+                    float g = tl[(cl + j) * FTOK + tok], up = tl[(64 + cl + j) * FTOK + tok];
+                    if (a.ss) {
+                        g = __fmul_rn(g, inv[tok]);
+                        up = __fmul_rn(up, inv[tok]);
                     }
+                    v[j] = __fmul_rn(g / (1.0f + expf(-g)), up);
                 }
-                uint32_t h0, m0, l0, h1, m1, l1;
-                split3(v[0], h0, m0, l0);
-                split3(v[1], h1, m1, l1);
-                H[j / 2] = h0 | (h1 << 16);
-                M[j / 2] = m0 | (m1 << 16);
-                L[j / 2] = l0 | (l1 << 16);
             }
-            const int ks = col0 / 32;
-            uint4* o = reinterpret_cast<uint4*>(a.frag_out + (size_t(ks) * 3 * 64 + ln) * 16);
-            o[0] = make_uint4(H[0], H[1], H[2], H[3]);
-            o[64] = make_uint4(M[0], M[1], M[2], M[3]);
-            o[128] = make_uint4(L[0], L[1], L[2], L[3]);
+            write_slot(tf, 2 * rb + ksl, ln, v);
         }
     } else {
-        // Output head: optional logits, per-token best (value, index) of this block.
-        if (a.out) {
-            for (int e = threadIdx.x; e < rows_wg * FTOK; e += nw * 64) {
-                const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-                if (tok < a.nt && row < W.rows) a.out[size_t(a.i0 + tok) * a.ldo + row] = tile[rl * FTOK + tok];
-            }
+        // Output head: logits, optional store, per-token best (value, index) of this block.
+        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
+            const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+            if (tok >= nt || row >= W.rows) continue;
+            const float v = a.ss ? __fmul_rn(tl[e], inv[tok]) : tl[e];
+            tl[e] = v;
+            if (a.out) a.out[size_t(ibase + tok) * a.ldo + a.row_base + row] = v;
         }
-        float* bv = inv + FTOK;               // [16 tokens][16 parts]
-        int* bi = reinterpret_cast<int*>(bv + FTOK * 16);
-        for (int e = threadIdx.x; e < FTOK * 16; e += nw * 64) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < FTOK * 16; e += nthr) {
             const int tok = e % FTOK, part = e / FTOK;
             float v = NAN;
             int ix = 0x7fffffff;
             for (int rl = part; rl < rows_wg; rl += 16) {
                 const int row = row0 + rl;
                 if (row >= W.rows) break;
-                const float x = tile[rl * FTOK + tok];
-                const bool xn = isnan(x), vn = isnan(v);
-                const bool take = (xn != vn) ? !xn : (xn ? row < ix : (x != v ? x > v : row < ix));
-                if (take) {
+                const float x = tl[rl * FTOK + tok];
+                if (beats(x, a.row_base + row, v, ix)) {
                     v = x;
                     ix = a.row_base + row;
                 }
@@ -528,124 +619,302 @@ __global__ __launch_bounds__(1024) void k_fused(FusedArgs a, FusedCfg cfg) {
             const int tok = threadIdx.x;
             float v = bv[tok * 16];
             int ix = bi[tok * 16];
-            for (int p = 1; p < 16; p++) {
-                const float x = bv[tok * 16 + p];
-                const int xi = bi[tok * 16 + p];
-                const bool xn = isnan(x), vn = isnan(v);
-                const bool take = (xn != vn) ? !xn : (xn ? xi < ix : (x != v ? x > v : xi < ix));
-                if (take) {
+            for (int q = 1; q < 16; q++) {
+                const float x = bv[tok * 16 + q];
+                const int xi = bi[tok * 16 + q];
+                if (beats(x, xi, v, ix)) {
                     v = x;
                     ix = xi;
                 }
             }
-            a.arg_val[blockIdx.x * FTOK + tok] = v;
-            a.arg_idx[blockIdx.x * FTOK + tok] = ix;
-            if (blockIdx.x == 0 && a.row0) a.row0[tok] = tile[tok];
+            const size_t at = (size_t(tile) * a.arg_stride + a.arg_off + rb) * FTOK + tok;
+            a.arg_val[at] = v;
+            a.arg_idx[at] = ix;
+            if (rb == 0 && a.row0) a.row0[ibase + tok] = tl[tok];
         }
     }
 }
 
-static size_t lds_bytes(const FusedCfg& c, int rows_wg) {
-    const size_t red = size_t(c.rg) * c.ksplit * 4 * 64 * 16;
-    const size_t region = size_t(c.frag_bytes) > red ? size_t(c.frag_bytes) : red;
-    return region + size_t(rows_wg) * FTOK * 4 + FTOK * 4 + FTOK * 16 * 8;
+// Output head, persistent: each workgroup copies the tile's fragments (every k-step) to LDS
+// once; its wavefronts then stream 64-row groups of the table over the whole K range, PF chunks
+// ahead, and reduce each group to logits and a per-token (value, index) argmax partial inside
+// the wavefront (lane l holds rows 16 r + 4 (l / 16) + i of token l % 16).
+constexpr int HEAD_WAVES = 8;
+// Chunks in flight per wavefront (int4 chunks carry four k-steps of fragments each).
+template <int BITS, bool G16>
+constexpr int head_pf() { return BITS == 4 ? (G16 ? 1 : 2) : 3; }
+
+template <int BITS, bool G16>
+__global__ __launch_bounds__(64 * HEAD_WAVES) void k_head(MMArgs a, int n_groups) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    constexpr int Q = Steps<BITS>::Q, HEAD_PF = head_pf<BITS, G16>();
+    const TMat& W = a.W;
+    const int tile = blockIdx.y, lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nt = min(FTOK, a.n - tile * FTOK), ibase = tile * FTOK;
+    const int nks = W.n_chunks * Q;
+    uint4* bl = reinterpret_cast<uint4*>(smem);
+    float* inv = reinterpret_cast<float*>(smem + size_t(nks) * 3 * 1024);
+
+    // This wavefront's groups: g = first + k * stride. Its first weight chunks go out at once.
+    const int stride = gridDim.x * HEAD_WAVES, first = blockIdx.x * HEAD_WAVES + wv;
+    const int my_groups = first < n_groups ? (n_groups - first + stride - 1) / stride : 0;
+    const int NC = W.n_chunks, F = my_groups * NC;
+    const size_t sst = size_t(NC) * 1024;
+    auto wbase = [&](int f) { return W.data + (size_t(4 * (first + (f / NC) * stride)) * NC * 64 + lane) * 16; };
+    uint4 raw[HEAD_PF][4];
+#pragma unroll
+    for (int p = 0; p < HEAD_PF; p++)
+        if (p < F) load_chunk(wbase(p), sst, p % NC, raw[p]);
+
+    const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
+    for (int i = threadIdx.x; i < nks * 3 * 64; i += blockDim.x) bl[i] = fb[i];
+    if (wv == 0) {
+        if (a.ss) inv_rms(a, tile, W.cols, inv);
+        else if (lane < FTOK) inv[lane] = 1.0f;
+    }
+    __syncthreads();
+
+    f32x4 total[4], acc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
+    float wbv = NAN;  // this wavefront's best (value, row) for token lane % 16 so far
+    int wbi = 0x7fffffff;
+    for (int f0 = 0; f0 < F; f0 += HEAD_PF) {
+#pragma unroll
+        for (int p = 0; p < HEAD_PF; p++) {
+            const int f = f0 + p;
+            if (f >= F) break;
+            const int c = f % NC;
+            const int g = first + (f / NC) * stride;
+            uint4 B[Q][3];
+#pragma unroll
+            for (int q = 0; q < Q; q++)
+#pragma unroll
+                for (int t = 0; t < 3; t++) B[q][t] = bl[((c * Q + q) * 3 + t) * 64 + lane];
+            chunk_mfma<BITS, G16>(W, 4 * g, c, 0, nks, B, raw[p], acc, total);
+            if (f + HEAD_PF < F) load_chunk(wbase(f + HEAD_PF), sst, (f + HEAD_PF) % NC, raw[p]);
+            if (c == NC - 1) {
+                // Group done: logits, optional store, argmax over its 64 rows per token.
+                const int tok = lane & 15;
+                const float iv = inv[tok];
+                float bvv = NAN;
+                int bix = 0x7fffffff;
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int row = 64 * g + 16 * r + 4 * (lane >> 4) + i;
+                        const float v = __fmul_rn(total[r][i], iv);
+                        if (row < W.rows) {
+                            if (a.out && tok < nt) a.out[size_t(ibase + tok) * a.ldo + a.row_base + row] = v;
+                            if (beats(v, a.row_base + row, bvv, bix)) {
+                                bvv = v;
+                                bix = a.row_base + row;
+                            }
+                        }
+                        if (row == 0 && a.row0) a.row0[ibase + tok] = v;
+                    }
+#pragma unroll
+                for (int o = 16; o < 64; o <<= 1) {
+                    const float ov = __shfl_xor(bvv, o, 64);
+                    const int oi = __shfl_xor(bix, o, 64);
+                    if (beats(ov, oi, bvv, bix)) {
+                        bvv = ov;
+                        bix = oi;
+                    }
+                }
+                if (beats(bvv, bix, wbv, wbi)) {
+                    wbv = bvv;
+                    wbi = bix;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) total[r] = f32x4{0, 0, 0, 0};
+            }
+        }
+    }
+    // One partial per workgroup: the best of its wavefronts, per token.
+    float* wv_v = reinterpret_cast<float*>(inv + FTOK);
+    int* wv_i = reinterpret_cast<int*>(wv_v + HEAD_WAVES * FTOK);
+    if (lane < FTOK) {
+        wv_v[wv * FTOK + lane] = wbv;
+        wv_i[wv * FTOK + lane] = wbi;
+    }
+    __syncthreads();
+    if (threadIdx.x < FTOK) {
+        const int tok = threadIdx.x;
+        float v = wv_v[tok];
+        int ix = wv_i[tok];
+        for (int w = 1; w < HEAD_WAVES; w++)
+            if (beats(wv_v[w * FTOK + tok], wv_i[w * FTOK + tok], v, ix)) {
+                v = wv_v[w * FTOK + tok];
+                ix = wv_i[w * FTOK + tok];
+            }
+        const size_t at = (size_t(tile) * a.arg_stride + a.arg_off + blockIdx.x) * FTOK + tok;
+        a.arg_val[at] = v;
+        a.arg_idx[at] = ix;
+    }
+}
+
+int device_cu_count() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        FCHECK(hipGetDevice(&dev));
+        FCHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    return cus;
+}
+
+constexpr size_t HEAD_LDS_MAX = 150 * 1024;
+
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens) {
+    MMPlan p;
+    p.rg = rg;
+    p.kw = kw < 1 ? 1 : kw;
+    const int cpw = 4 / (W.bits == 16 ? 1 : (W.bits == 8 ? 2 : 4));
+    const int waves_k = (W.n_chunks + cpw - 1) / cpw;  // wavefront shares along K
+    if (p.kw > waves_k) p.kw = waves_k;
+    if (p.rg > 8) throw std::runtime_error("a matrix workgroup holds at most 8 wavefronts");
+    if (p.rg * p.kw > 8) p.kw = 8 / p.rg;
+    p.nsplit = (waves_k + p.kw - 1) / p.kw;
+    while (p.nsplit > MAX_SPLIT && p.rg * (p.kw + 1) <= 8) {
+        p.kw++;
+        p.nsplit = (waves_k + p.kw - 1) / p.kw;
+    }
+    if (p.nsplit > MAX_SPLIT) throw std::runtime_error("matrix too wide for the split-K limit");
+    const int groups = W.n_strips / 4;
+    if (groups % rg) throw std::runtime_error("matrix rows do not fill whole row blocks");
+    p.nrb = groups / rg;
+    p.tiles = (n_tokens + FTOK - 1) / FTOK;
+    return p;
+}
+
+size_t mm_part_floats(const MMPlan& p) {
+    return p.nsplit > 1 ? size_t(p.tiles) * p.nrb * p.nsplit * 64 * p.rg * FTOK : 0;
+}
+size_t mm_counters(const MMPlan& p) { return p.nsplit > 1 ? size_t(p.tiles) * p.nrb : 0; }
+
+static size_t lds_bytes(const MMPlan& p) {
+    const size_t red = p.kw > 1 ? size_t(p.rg) * p.kw * 4 * 64 * 16 : 0;
+    const size_t rows = size_t(64 * p.rg);
+    return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX) * 4;
 }
 
 template <int EPI>
-static void launch(const FusedArgs& a, FusedCfg cfg, int nblocks, hipStream_t s) {
-    const int rows_wg = 64 * cfg.rg;
-    const size_t lds = lds_bytes(cfg, rows_wg);
-    const dim3 grid(nblocks), block(64 * cfg.rg * cfg.ksplit);
+static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    if (p.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
+    const dim3 grid(p.nrb * p.nsplit, p.tiles), block(64 * p.rg * p.kw);
+    const size_t lds = lds_bytes(p);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
     switch (a.W.bits) {
-        case 16: hipLaunchKernelGGL((k_fused<16, EPI, false>), grid, block, lds, s, a, cfg); break;
+        case 16: hipLaunchKernelGGL((k_mm<16, EPI, false>), grid, block, lds, s, a, p, sc); break;
         case 8:
-            if (g16) hipLaunchKernelGGL((k_fused<8, EPI, true>), grid, block, lds, s, a, cfg);
-            else hipLaunchKernelGGL((k_fused<8, EPI, false>), grid, block, lds, s, a, cfg);
+            if (g16) hipLaunchKernelGGL((k_mm<8, EPI, true>), grid, block, lds, s, a, p, sc);
+            else hipLaunchKernelGGL((k_mm<8, EPI, false>), grid, block, lds, s, a, p, sc);
             break;
         default:
-            if (g16) hipLaunchKernelGGL((k_fused<4, EPI, true>), grid, block, lds, s, a, cfg);
-            else hipLaunchKernelGGL((k_fused<4, EPI, false>), grid, block, lds, s, a, cfg);
+            if (g16) hipLaunchKernelGGL((k_mm<4, EPI, true>), grid, block, lds, s, a, p, sc);
+            else hipLaunchKernelGGL((k_mm<4, EPI, false>), grid, block, lds, s, a, p, sc);
             break;
     }
     FCHECK(hipGetLastError());
 }
 
-constexpr int FRAG_LDS_MAX = 96 * 1024;
-
-static FusedCfg make_cfg(const FusedArgs& a, int rg, int ksplit) {
-    FusedCfg c;
-    c.rg = rg;
-    c.ksplit = ksplit < 1 ? 1 : (ksplit > a.W.n_chunks ? a.W.n_chunks : ksplit);
-    while (c.rg * c.ksplit > 16) c.ksplit--;
-    const int fb = tile_kpad(a.W.cols) / 32 * 3 * 1024;
-    c.frag_lds = a.frags == nullptr ? 1 : 0;
-    if (c.frag_lds && fb > FRAG_LDS_MAX) throw std::runtime_error("fused kernel: input too wide for LDS fragments");
-    c.frag_bytes = c.frag_lds ? fb : 0;
-    return c;
+void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    if (64 * p.rg % a.hd) throw std::runtime_error("q/k/v row blocks must hold whole heads");
+    if (a.hd / 2 > ROPE_HALF_MAX) throw std::runtime_error("head_dim too large");
+    launch<EPI_QKV>(a, p, sc, s);
+}
+void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) { launch<EPI_RESID>(a, p, sc, s); }
+void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    if (p.rg != 2) throw std::runtime_error("gate|up runs in 128-row blocks");
+    launch<EPI_SILU>(a, p, sc, s);
+}
+int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES * FTOK * 8;
+    if (p.rg != 1 || lds > HEAD_LDS_MAX) {
+        launch<EPI_HEAD>(a, p, sc, s);
+        return p.nrb;
+    }
+    // One workgroup of HEAD_WAVES wavefronts per CU (the fragments fill most of its LDS).
+    const int n_groups = p.nrb;
+    const int blocks = std::min(device_cu_count(), (n_groups + HEAD_WAVES - 1) / HEAD_WAVES);
+    const dim3 grid(blocks, p.tiles), block(64 * HEAD_WAVES);
+    const bool g16 = a.W.bits != 16 && a.W.group == 16;
+    switch (a.W.bits) {
+        case 16: hipLaunchKernelGGL((k_head<16, false>), grid, block, lds, s, a, n_groups); break;
+        case 8:
+            if (g16) hipLaunchKernelGGL((k_head<8, true>), grid, block, lds, s, a, n_groups);
+            else hipLaunchKernelGGL((k_head<8, false>), grid, block, lds, s, a, n_groups);
+            break;
+        default:
+            if (g16) hipLaunchKernelGGL((k_head<4, true>), grid, block, lds, s, a, n_groups);
+            else hipLaunchKernelGGL((k_head<4, false>), grid, block, lds, s, a, n_groups);
+            break;
+    }
+    FCHECK(hipGetLastError());
+    return blocks;
 }
 
-void fused_qkv(const FusedArgs& a, hipStream_t s) {
-    const int rg = a.hd > 64 ? a.hd / 64 : 1;
-    FusedCfg c = make_cfg(a, rg, 16 / rg);
-    launch<EPI_QKV>(a, c, (a.W.rows + 64 * rg - 1) / (64 * rg), s);
-}
-
-void fused_residual(const FusedArgs& a, int ksplit, hipStream_t s) {
-    FusedCfg c = make_cfg(a, 1, ksplit);
-    launch<EPI_RESID>(a, c, (a.W.rows + 63) / 64, s);
-}
-
-void fused_gate_up(const FusedArgs& a, hipStream_t s) {
-    FusedCfg c = make_cfg(a, 2, 8);
-    launch<EPI_SILU>(a, c, a.W.rows / 128, s);
-}
-
-constexpr int HEAD_RG = 4;
-int fused_head_blocks(const TMat& E) { return (E.rows + 64 * HEAD_RG - 1) / (64 * HEAD_RG); }
-
-void fused_head(const FusedArgs& a, hipStream_t s) {
-    FusedCfg c = make_cfg(a, HEAD_RG, 2);
-    launch<EPI_HEAD>(a, c, fused_head_blocks(a.W), s);
-}
-
-__device__ __forceinline__ bool beats2(float va, int ia, float vb, int ib) {
-    const bool an = isnan(va), bn = isnan(vb);
-    if (an != bn) return !an;
-    if (an) return ia < ib;
-    if (va != vb) return va > vb;
-    return ia < ib;
-}
-
-// One wavefront per token: lane-strided scan of the block partials, then a shuffle tree.
-__global__ void k_head_final(const float* __restrict__ pv, const int* __restrict__ pi, int nblocks,
-                             const float* __restrict__ row0, int i0, uint32_t* __restrict__ amax) {
-    const int tok = blockIdx.x, lane = threadIdx.x;
+// One workgroup per token: every thread loads its share of the partials at once, then a shuffle
+// tree per wavefront and a scan over the wavefronts (the order does not matter: `beats` is a
+// total order).
+__global__ __launch_bounds__(256) void k_head_final(const float* __restrict__ pv, const int* __restrict__ pi, int arg_stride,
+                                                    int nblocks, const float* __restrict__ row0, uint32_t* __restrict__ amax) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int i = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const size_t base = size_t(i / FTOK) * arg_stride * FTOK + i % FTOK;
     float v = NAN;
     int ix = 0x7fffffff;
-    for (int b = lane; b < nblocks; b += 64) {
-        const float x = pv[b * FTOK + tok];
-        const int xi = pi[b * FTOK + tok];
-        if (beats2(x, xi, v, ix)) {
-            v = x;
-            ix = xi;
+    for (int b0 = threadIdx.x; b0 < nblocks; b0 += 8 * 256) {
+        float xv[8];
+        int xi[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int b = b0 + 256 * u;
+            xv[u] = NAN;
+            xi[u] = 0x7fffffff;
+            if (b < nblocks) {
+                xv[u] = pv[base + size_t(b) * FTOK];
+                xi[u] = pi[base + size_t(b) * FTOK];
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (beats(xv[u], xi[u], v, ix)) {
+                v = xv[u];
+                ix = xi[u];
+            }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(v, o, 64);
         const int oi = __shfl_xor(ix, o, 64);
-        if (beats2(ov, oi, v, ix)) {
+        if (beats(ov, oi, v, ix)) {
             v = ov;
             ix = oi;
         }
     }
-    if (lane == 0) amax[i0 + tok] = isnan(row0[tok]) ? 0u : uint32_t(ix);
+    if (lane == 0) {
+        sv[w] = v;
+        si[w] = ix;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++)
+            if (beats(sv[k], si[k], v, ix)) {
+                v = sv[k];
+                ix = si[k];
+            }
+        amax[i] = isnan(row0[i]) ? 0u : uint32_t(ix);
+    }
 }
 
-void head_argmax_final(const float* pv, const int* pi, int nblocks, const float* row0, int i0, int nt, uint32_t* amax,
+void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
                        hipStream_t s) {
-    hipLaunchKernelGGL(k_head_final, dim3(nt), dim3(64), 0, s, pv, pi, nblocks, row0, i0, amax);
+    hipLaunchKernelGGL(k_head_final, dim3(n), dim3(256), 0, s, pv, pi, arg_stride, nblocks, row0, amax);
     FCHECK(hipGetLastError());
 }
 

@@ -5,9 +5,16 @@
 // that a wavefront load of one chunk of one strip is 1 KiB of contiguous memory and each lane
 // receives exactly the A operand of v_mfma_f32_16x16x32_bf16 for its row and k-block. A chunk
 // covers 32 columns for bf16, 64 for int8 and 128 for int4. Scales are [strip][group][16 rows]
-// bf16. Inputs reach the MFMA B operand as three bf16 terms whose sum is the f32 value exactly
-// ("B fragments", [k-step][term][64 lanes][16 B]), so every product is exact and accumulation is
-// f32.
+// bf16.
+//
+// Activations reach the MFMA B operand as "fragments": three bf16 terms whose sum is the f32
+// value exactly, stored per tile of 16 tokens as [k-step][term][64 lanes][16 B] (lane l holds
+// token l % 16, columns 32 k-step + 8 (l / 16) + [0, 8)). Every matrix input is written in this
+// form by the kernel that produces it (embedding, attention, the residual and SiLU epilogues), so
+// the matrix kernels start streaming weights at once. Inputs that the reference RMS-normalises
+// are stored as x * w; the per-token 1 / rms is applied to the matrix output in the epilogue,
+// from sum-of-squares partials (one per 64 columns, [tile][slot][16 tokens]) that the producer
+// writes beside the fragments.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,11 +34,11 @@ struct TMat {
     int n_groups = 0;   // groups per row, padding columns included
 };
 
-constexpr int FTOK = 16;  // tokens per launch tile (the MFMA N dimension)
+constexpr int FTOK = 16;  // tokens per tile (the MFMA N dimension)
 
 __host__ __device__ inline int tile_chunk_cols(int bits) { return bits == 16 ? 32 : (bits == 8 ? 64 : 128); }
 __host__ __device__ inline int tile_kpad(int cols) { return (cols + 127) / 128 * 128; }
-// Rows are padded to a multiple of row_align (64, or 256 for the output head's 256-row blocks).
+// Rows are padded to a multiple of row_align.
 TMat tile_shape(int bits, int group, int rows, int cols, int row_align = 64);
 size_t tile_data_bytes(const TMat& m);
 size_t tile_scale_bytes(const TMat& m);
@@ -42,24 +49,29 @@ void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int
 // Initialise padding: zero-weight bytes and zero scales over the whole matrix.
 void tile_clear(const TMat& m, hipStream_t s);
 
-// Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization).
-void tile_embed(const TMat& E, const uint32_t* tokens, int t, float* x, hipStream_t s);
+// Bytes of one token tile of fragments for `cols` input columns.
+__host__ __device__ inline size_t frag_tile_bytes(int cols) { return size_t(tile_kpad(cols)) / 32 * 3 * 1024; }
+// Sum-of-squares slots (64 columns each) of a row of `cols` values.
+__host__ __device__ inline int ss_slots(int cols) { return (cols + 63) / 64; }
 
-// B fragments of x rows [i0, i0 + nt) (f32, row stride ldx), optionally RMS-normalised with w,
-// written to global memory (kpad / 32 k-steps x 3 KiB).
-void frag_build(const float* x, int ldx, int i0, int nt, int cols, const float* w, float eps, uint8_t* frags, hipStream_t s);
+// Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization) into
+// x [n][cols], plus fragments of x * w and sum-of-squares partials.
+void tile_embed(const TMat& E, const uint32_t* tokens, int n, float* x, const float* w, uint8_t* frags, float* ss,
+                hipStream_t s);
+// Fragments (of x * w, or of x when w is null) and sum-of-squares partials (when ss is not null)
+// of rows [0, n) of x [n][cols].
+void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, float* ss, hipStream_t s);
 
-struct FusedArgs {
-    // weights
+struct MMArgs {
     TMat W;
-    // input: f32 rows (x) with optional RMSNorm weights, or prebuilt B fragments
-    const float* x = nullptr;
-    int ldx = 0;
-    const float* norm = nullptr;
-    float eps = 0;
+    // input: fragments, tile stride frag_stride; optional RMSNorm (1 / rms from ss partials)
     const uint8_t* frags = nullptr;
-    int i0 = 0, nt = 0;  // token tile
-    // epilogue data
+    size_t frag_stride = 0;
+    const float* ss = nullptr;
+    int ss_slots = 0;
+    float eps = 0;
+    int n = 0;  // tokens of the launch (tiles of 16)
+    // epilogue
     const float* bias = nullptr;
     float* out = nullptr;  // q rows / residual rows / logits
     int ldo = 0;
@@ -67,26 +79,54 @@ struct FusedArgs {
     float* vcache = nullptr;
     const float* rope_cos = nullptr;
     const float* rope_sin = nullptr;
-    const int* pos0 = nullptr;  // device scalar: position of token 0 of the step
+    const int* pos0 = nullptr;  // device scalar: position of token 0 of the launch
     int heads = 0, kv_heads = 0, hd = 0;
-    uint8_t* frag_out = nullptr;  // SiLU epilogue: act fragments
-    float* arg_val = nullptr;     // argmax epilogue partials [block][16]
+    // output fragments and sum-of-squares partials (residual: of x * onorm; SiLU: of act)
+    uint8_t* ofrags = nullptr;
+    size_t ofrag_stride = 0;
+    const float* onorm = nullptr;
+    float* oss = nullptr;
+    int oss_slots = 0;
+    // head: per-block argmax partials [tile][arg_stride][16], block index arg_off + block
+    float* arg_val = nullptr;
     int* arg_idx = nullptr;
-    int row_base = 0;             // added to argmax row indices
-    float* row0 = nullptr;        // head: logits of row 0 of this launch, per token
+    int arg_stride = 0, arg_off = 0;
+    int row_base = 0;       // added to argmax row indices
+    float* row0 = nullptr;  // logits of row 0 per token ([tile * 16 + token]), when set
 };
 
-// QKV projection + bias + RoPE + K/V append (norm prologue). Rows: q heads, k heads, v heads.
-void fused_qkv(const FusedArgs& a, hipStream_t s);
-// y = W x, x[row] += y (norm-free prologue from f32 rows, or fragments).
-void fused_residual(const FusedArgs& a, int ksplit, hipStream_t s);
-// gate|up projection (row blocks of 64 interleaved gate, up) + SiLU(g) * u -> act fragments.
-void fused_gate_up(const FusedArgs& a, hipStream_t s);
-// Output head: logits of 256-row blocks, per-block argmax partials, optional logits store.
-void fused_head(const FusedArgs& a, hipStream_t s);
-int fused_head_blocks(const TMat& E);
-// Final argmax over head-block partials (src/spec.rs:41-49 rule); row0 holds logits[.][0].
-void head_argmax_final(const float* pv, const int* pi, int nblocks, const float* row0, int i0, int nt, uint32_t* amax,
+// Work split of one launch: each workgroup owns rg groups of 64 rows and one of nsplit K ranges,
+// cut among kw wavefronts per row group. With nsplit > 1 the pieces meet in `part` and the last
+// workgroup of a row block to finish adds them in split order (counters in `cnt` start at zero
+// and are left at zero).
+struct MMPlan {
+    int rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
+};
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens);
+size_t mm_part_floats(const MMPlan& p);
+size_t mm_counters(const MMPlan& p);
+
+// Compute units of the current device (cached after the first call).
+int device_cu_count();
+
+struct MMScratch {
+    float* part = nullptr;
+    int* cnt = nullptr;
+};
+
+// QKV projection + 1/rms + bias + RoPE + K/V append. Rows: q heads, k heads, v heads.
+void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// x[row] += W x; then fragments of x * onorm and sum-of-squares partials of the new rows.
+void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// gate|up projection (row blocks of 64 interleaved gate, up; plan.rg == 2) + 1/rms +
+// SiLU(g) * u -> act fragments.
+void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// Output head: logits (1/rms applied), optional logits store, argmax partials at
+// [tile][arg_off + b][16] for b below the returned count.
+int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// Final argmax over head-block partials (src/spec.rs:41-49 rule) for n tokens; row0 holds
+// logits[.][0].
+void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
                        hipStream_t s);
 
 }  // namespace ls

@@ -16,6 +16,8 @@
 
 #include <chrono>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 
 namespace ls {
 
@@ -178,7 +180,10 @@ public:
     }
     void release_head_chunk(size_t) override {}
     void end_forward() override {}
-    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x) override { tile_embed(E_, dev_tokens, t, x, s_); }
+    bool resident() const override { return true; }
+    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x, const float* w, uint8_t* frags, float* ss) override {
+        tile_embed(E_, dev_tokens, t, x, w, frags, ss, s_);
+    }
     ls_report report() const override {
         ls_report r{};
         r.resident_weight_bytes = arena_.n + edata_.n + escales_.n;
@@ -291,7 +296,8 @@ public:
             fail("forward pass ended before every scheduled item was consumed", LS_E_STATE);
     }
 
-    void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x) override {
+    bool resident() const override { return false; }
+    void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x, const float* w, uint8_t* frags, float* ss) override {
         // Rows come from the source on every pass, as src/provider.rs:284-286.
         const size_t rb = c_.row_bytes();
         HIPC(hipEventSynchronize(embed_copied_));
@@ -299,6 +305,7 @@ public:
         HIPC(hipMemcpyAsync(embed_raw_.p, embed_stage_.p, size_t(t) * rb, hipMemcpyHostToDevice, compute_));
         HIPC(hipEventRecord(embed_copied_, compute_));
         embed_raw_rows(embed_raw_.as<uint8_t>(), c_.embed_format.bits, c_.embed_format.group, int(c_.hidden), t, x, compute_);
+        if (frags) x_frags(x, t, int(c_.hidden), w, frags, ss, compute_);
     }
 
     ls_report report() const override {
@@ -399,7 +406,6 @@ std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStr
 // Model
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
-constexpr size_t FRAG_LDS_LIMIT = 96 * 1024;
 constexpr int MAX_TILES = int(PREFILL_CHUNK) / FTOK;
 
 Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
@@ -407,9 +413,10 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     if (max_ctx == 0) fail("max_ctx must be positive");
     const Config& c = cfg_;
     if (c.inter % 64 != 0) fail("the intermediate size must be a multiple of 64");
-    if (c.head_dim > 256 || 256 % c.head_dim != 0) fail("head_dim must divide 256");
-    if (c.head_dim > 64 && c.head_dim % 64 != 0) fail("head_dim above 64 must be a multiple of 64");
+    if (c.head_dim != 16 && c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128)
+        fail("head_dim must be 16, 32, 64 or 128");
     HIPC(hipSetDevice(device));
+    (void)device_cu_count();  // cached before any graph capture
     HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     HIPC(hipEventCreate(&ev0_));
     HIPC(hipEventCreate(&ev1_));
@@ -443,19 +450,56 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     HIPC(hipMemcpy(fnorm_.p, src.final_norm().data(), h * 4, hipMemcpyHostToDevice));
 
     vpad_ = (c.vocab + 63) / 64 * 64;
-    head_blocks_ = fused_head_blocks(tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256));
-    act_frag_bytes_ = size_t(tile_kpad(int(in))) / 32 * 3 * 1024;
+    if (c.hidden % 8) fail("hidden size must be a multiple of 8");
+    const size_t hq = c.heads * c.head_dim;
+    fb_h_ = frag_tile_bytes(int(h));
+    fb_q_ = frag_tile_bytes(int(hq));
+    fb_in_ = frag_tile_bytes(int(in));
+    slots_h_ = ss_slots(int(h));
+    if (h > 4096) fail("hidden sizes above 4096 are not supported");
+    {
+        const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
+        const size_t n_chunks = (c.vocab + HEAD_ROWS - 1) / HEAD_ROWS;
+        head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * HEAD_ROWS / 64));
+    }
+    plan_kw_from_env();
     x_ = DevBuf(T * h * 4);
-    q_ = DevBuf(T * h * 4);
-    attn_ = DevBuf(T * h * 4);
-    act_frags_ = DevBuf(act_frag_bytes_ * MAX_TILES);
-    HIPC(hipMemsetAsync(act_frags_.p, 0, act_frags_.n, stream_));  // padding columns stay zero
-    in_frags_ = DevBuf(size_t(tile_kpad(int(h))) / 32 * 3 * 1024);
-    head_frags_ = DevBuf(size_t(tile_kpad(int(h))) / 32 * 3 * 1024 * MAX_TILES);
+    q_ = DevBuf(T * hq * 4);
+    // Fragment buffers start at zero: padding columns are never written and must stay finite.
+    xf_ = DevBuf(fb_h_ * MAX_TILES);
+    ss_ = DevBuf(size_t(MAX_TILES) * slots_h_ * FTOK * 4);
+    af_ = DevBuf(fb_q_ * MAX_TILES);
+    actf_ = DevBuf(fb_in_ * MAX_TILES);
+    HIPC(hipMemsetAsync(xf_.p, 0, xf_.n, stream_));
+    HIPC(hipMemsetAsync(ss_.p, 0, ss_.n, stream_));
+    HIPC(hipMemsetAsync(af_.p, 0, af_.n, stream_));
+    HIPC(hipMemsetAsync(actf_.p, 0, actf_.n, stream_));
+    {
+        // Split-K scratch for the largest launch of each matrix (PREFILL_CHUNK tokens).
+        const LayerArena la = layer_arena(c);
+        const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
+        const int n = int(T);
+        const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(HEAD_ROWS), int(h), 256);
+        const MMPlan plans[] = {mm_plan(la.qkv, qkv_rg(), kw_qkv_, n), mm_plan(la.o, 1, kw_o_, n),
+                                mm_plan(la.gu, 2, kw_gu_, n),           mm_plan(la.down, 1, kw_down_, n),
+                                mm_plan(e_res, 1, kw_head_, n),         mm_plan(e_chunk, 1, kw_head_, n)};
+        size_t pf = 0, nc = 0;
+        for (const MMPlan& pl : plans) {
+            pf = std::max(pf, mm_part_floats(pl));
+            nc = std::max(nc, mm_counters(pl));
+        }
+        part_ = DevBuf(std::max<size_t>(pf, 1) * 4);
+        cnt_ = DevBuf(std::max<size_t>(nc, 1) * 4);
+        HIPC(hipMemsetAsync(cnt_.p, 0, cnt_.n, stream_));
+    }
     attn_scratch_ = DevBuf(attention_scratch_floats(int(T), int(c.heads), int(c.head_dim), int(max_ctx)) * 4);
+    attn_splits_ = attention_splits(int(max_ctx));
+    attn_cnt_ = DevBuf(size_t(MAX_TILES) * c.heads * 4);
+    HIPC(hipMemsetAsync(attn_cnt_.p, 0, attn_cnt_.n, stream_));
     logits_ = DevBuf(T * vpad_ * 4);
-    hpv_ = DevBuf(size_t(MAX_TILES) * (head_blocks_ + 1) * FTOK * 4);
-    hpi_ = DevBuf(size_t(MAX_TILES) * (head_blocks_ + 1) * FTOK * 4);
+    hpv_ = DevBuf(size_t(MAX_TILES) * head_blocks_ * FTOK * 4);
+    hpi_ = DevBuf(size_t(MAX_TILES) * head_blocks_ * FTOK * 4);
+    row0_ = DevBuf(T * 4);
     amax_ = DevBuf(T * 4);
     tok_ = DevBuf(max_ctx * 4);
     acc_ = DevBuf(16);
@@ -468,6 +512,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
 
 Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
     for (hipEvent_t e : prof_ev_) (void)hipEventDestroy(e);
     prov_.reset();
     if (ev0_) (void)hipEventDestroy(ev0_);
@@ -520,6 +565,11 @@ void Model::harvest() {
     prof_used_ = 0;
 }
 
+void Model::set_graphs(bool on) {
+    HIPC(hipStreamSynchronize(stream_));
+    graphs_on_ = on;
+}
+
 void Model::set_profiling(bool on) {
     HIPC(hipStreamSynchronize(stream_));
     harvest();
@@ -535,10 +585,19 @@ ls_kernel_stat Model::read_profile() {
     return r;
 }
 
-const uint8_t* Model::global_frags(const float* x, int i0, int nt, int cols, const float* w) {
-    if (size_t(tile_kpad(cols)) / 32 * 3 * 1024 <= FRAG_LDS_LIMIT) return nullptr;
-    frag_build(x, int(cfg_.hidden), i0, nt, cols, w, cfg_.eps, in_frags_.as<uint8_t>(), stream_);
-    return in_frags_.as<uint8_t>();
+// Workgroup shapes along K can be overridden for tuning: LS_MM_KW="qkv,o,gate_up,down,head".
+void Model::plan_kw_from_env() {
+    const char* e = std::getenv("LS_MM_KW");
+    if (!e || !*e) return;
+    int v[5];
+    if (std::sscanf(e, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) != 5) fail("LS_MM_KW needs five integers");
+    for (int x : v)
+        if (x < 1 || x > 8) fail("LS_MM_KW values must be between 1 and 8");
+    kw_qkv_ = v[0];
+    kw_o_ = v[1];
+    kw_gu_ = v[2];
+    kw_down_ = v[3];
+    kw_head_ = v[4];
 }
 
 // Copy a call's tokens (and the position of each 128-token chunk) to the device once. The
@@ -556,30 +615,38 @@ const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
 void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits) {
     const Config& c = cfg_;
     const int h = int(c.hidden), kv = int(c.kv_dim()), T = int(t);
-    const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim), pos0 = int(pos_);
+    const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim);
+    const int hq = heads * hd;
     hipStream_t s = stream_;
     float* x = x_.as<float>();
+    float* ss = ss_.as<float>();
+    uint8_t* xf = xf_.as<uint8_t>();
     const int* pos_dev = pos_dev_.as<int>() + chunk_index_;  // this chunk's first position
-    prov_->embed(tok, dtok, T, x);
+    const MMScratch scr{part_.as<float>(), cnt_.as<int>()};
+    const bool res = prov_->resident();
     prov_->begin_forward(n_logits > 0);
+    // Resident layers: the embedding kernel and every down epilogue write the fragments of the
+    // next layer's input directly. Streamed layers: each layer's fragments are made once it has
+    // arrived.
+    const DevLayer* L0 = res ? &prov_->layer(0) : nullptr;
+    prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr);
     for (size_t l = 0; l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
         float* kc = kcache_.as<float>() + l * max_ctx_ * kv;
         float* vc = vcache_.as<float>() + l * max_ctx_ * kv;
-        for (int i0 = 0; i0 < T; i0 += FTOK) {
-            const int nt = std::min(FTOK, T - i0);
-            FusedArgs a;
+        if (!res) x_frags(x, T, h, L.in_norm, xf, ss, s);
+        {
+            MMArgs a;
             a.W = L.qkv;
-            a.x = x;
-            a.ldx = h;
-            a.norm = L.in_norm;
+            a.frags = xf;
+            a.frag_stride = fb_h_;
+            a.ss = ss;
+            a.ss_slots = slots_h_;
             a.eps = c.eps;
-            a.frags = global_frags(x, i0, nt, h, L.in_norm);
-            a.i0 = i0;
-            a.nt = nt;
+            a.n = T;
             a.bias = L.b_qkv;
             a.out = q_.as<float>();
-            a.ldo = h;
+            a.ldo = hq;
             a.kcache = kc;
             a.vcache = vc;
             a.rope_cos = rope_cos_.as<float>();
@@ -589,97 +656,98 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.kv_heads = kvh;
             a.hd = hd;
             prof_begin();
-            fused_qkv(a, s);
-            prof_end(L.qkv, nt);
+            mm_qkv(a, mm_plan(L.qkv, qkv_rg(), kw_qkv_, T), scr, s);
+            prof_end(L.qkv, T);
         }
-        attention(q_.as<float>(), h, T, heads, kvh, hd, pos0, int(max_ctx_), kc, vc, attn_scratch_.as<float>(), attn_.as<float>(), s);
-        for (int i0 = 0; i0 < T; i0 += FTOK) {
-            const int nt = std::min(FTOK, T - i0);
-            FusedArgs a;
+        attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, int(max_ctx_), kc, vc, attn_scratch_.as<float>(), attn_cnt_.as<int>(),
+                  attn_splits_, af_.as<uint8_t>(), s);
+        {
+            MMArgs a;
             a.W = L.o;
-            a.x = attn_.as<float>();
-            a.ldx = h;
-            a.frags = global_frags(attn_.as<float>(), i0, nt, h, nullptr);
-            a.i0 = i0;
-            a.nt = nt;
+            a.frags = af_.as<uint8_t>();
+            a.frag_stride = fb_q_;
+            a.n = T;
             a.out = x;
             a.ldo = h;
+            a.ofrags = xf;
+            a.ofrag_stride = fb_h_;
+            a.onorm = L.post_norm;
+            a.oss = ss;
+            a.oss_slots = slots_h_;
             prof_begin();
-            fused_residual(a, 16, s);
-            prof_end(L.o, nt);
+            mm_residual(a, mm_plan(L.o, 1, kw_o_, T), scr, s);
+            prof_end(L.o, T);
         }
-        for (int i0 = 0; i0 < T; i0 += FTOK) {
-            const int nt = std::min(FTOK, T - i0);
-            uint8_t* af = act_frags_.as<uint8_t>() + size_t(i0 / FTOK) * act_frag_bytes_;
-            FusedArgs a;
+        {
+            MMArgs a;
             a.W = L.gu;
-            a.x = x;
-            a.ldx = h;
-            a.norm = L.post_norm;
+            a.frags = xf;
+            a.frag_stride = fb_h_;
+            a.ss = ss;
+            a.ss_slots = slots_h_;
             a.eps = c.eps;
-            a.frags = global_frags(x, i0, nt, h, L.post_norm);
-            a.i0 = i0;
-            a.nt = nt;
-            a.frag_out = af;
+            a.n = T;
+            a.ofrags = actf_.as<uint8_t>();
+            a.ofrag_stride = fb_in_;
             prof_begin();
-            fused_gate_up(a, s);
-            prof_end(L.gu, nt);
-            FusedArgs d;
-            d.W = L.down;
-            d.frags = af;
-            d.i0 = i0;
-            d.nt = nt;
-            d.out = x;
-            d.ldo = h;
+            mm_gate_up(a, mm_plan(L.gu, 2, kw_gu_, T), scr, s);
+            prof_end(L.gu, T);
+        }
+        {
+            const bool last = l + 1 == c.layers;
+            MMArgs a;
+            a.W = L.down;
+            a.frags = actf_.as<uint8_t>();
+            a.frag_stride = fb_in_;
+            a.n = T;
+            a.out = x;
+            a.ldo = h;
+            if (last || res) {
+                a.ofrags = xf;
+                a.ofrag_stride = fb_h_;
+                a.onorm = last ? fnorm_.as<float>() : prov_->layer(l + 1).in_norm;
+                a.oss = ss;
+                a.oss_slots = slots_h_;
+            }
             prof_begin();
-            fused_residual(d, 16, s);
-            prof_end(L.down, nt);
+            mm_residual(a, mm_plan(L.down, 1, kw_down_, T), scr, s);
+            prof_end(L.down, T);
         }
         prov_->release_layer(l);
     }
     if (n_logits > 0) {
-        // Head (src/model.rs:190-216): final RMSNorm of the last n rows in the prologue, the tied
-        // table (one chunk when resident), per-block argmax partials, then the argmax.
-        const int n = int(n_logits);
-        const float* xh = x + size_t(T - n) * h;
-        float* logits = logits_.as<float>();
-        const size_t tile_stride = size_t(head_blocks_ + 1) * FTOK;
-        const size_t fb = size_t(tile_kpad(h)) / 32 * 3 * 1024;
-        // B fragments of the final-normed rows, once per token tile, read by every head block.
-        for (int i0 = 0; i0 < n; i0 += FTOK)
-            frag_build(xh, h, i0, std::min(FTOK, n - i0), h, fnorm_.as<float>(), c.eps, head_frags_.as<uint8_t>() + size_t(i0 / FTOK) * fb, s);
+        // Head (src/model.rs:190-216) over the token tiles holding the last n rows: the tied table
+        // (one chunk when resident), per-block argmax partials, then the argmax. The final norm
+        // was applied by the last layer's epilogue (fragments of x * w, 1 / rms here).
+        const int t0 = (T - int(n_logits)) / FTOK, nh = T - FTOK * t0;
+        head_off_ = size_t(T) - n_logits - size_t(FTOK) * t0;
+        int blocks = 0;  // argmax partials written by this pass
         for (size_t ci = 0; ci < prov_->n_head_chunks(); ci++) {
             HeadChunk hc = prov_->head_chunk(ci);
-            for (int i0 = 0; i0 < n; i0 += FTOK) {
-                const int nt = std::min(FTOK, n - i0);
-                const size_t toff = size_t(i0 / FTOK) * tile_stride;
-                FusedArgs a;
-                a.W = hc.mat;
-                a.x = xh;
-                a.ldx = h;
-                a.norm = fnorm_.as<float>();
-                a.eps = c.eps;
-                a.frags = head_frags_.as<uint8_t>() + size_t(i0 / FTOK) * fb;
-                a.i0 = i0;
-                a.nt = nt;
-                a.out = want_logits ? logits + hc.first : nullptr;
-                a.ldo = int(vpad_);
-                a.arg_val = hpv_.as<float>() + toff + (hc.first / 256) * FTOK;
-                a.arg_idx = hpi_.as<int>() + toff + (hc.first / 256) * FTOK;
-                a.row_base = int(hc.first);
-                a.row0 = hc.first == 0 ? hpv_.as<float>() + toff + size_t(head_blocks_) * FTOK : nullptr;
-                prof_begin();
-                fused_head(a, s);
-                prof_end(hc.mat, nt);
-            }
+            MMArgs a;
+            a.W = hc.mat;
+            a.frags = xf + size_t(t0) * fb_h_;
+            a.frag_stride = fb_h_;
+            a.ss = ss + size_t(t0) * slots_h_ * FTOK;
+            a.ss_slots = slots_h_;
+            a.eps = c.eps;
+            a.n = nh;
+            a.out = want_logits ? logits_.as<float>() : nullptr;
+            a.ldo = int(vpad_);
+            a.arg_val = hpv_.as<float>();
+            a.arg_idx = hpi_.as<int>();
+            a.arg_stride = head_blocks_;
+            a.arg_off = blocks;
+            a.row_base = int(hc.first);
+            a.row0 = hc.first == 0 ? row0_.as<float>() : nullptr;
+            const MMPlan plan = mm_plan(hc.mat, 1, kw_head_, nh);
+            if (a.arg_off + plan.nrb > head_blocks_) fail("head blocks exceed the argmax buffer", LS_E_STATE);
+            prof_begin();
+            blocks += mm_head(a, plan, scr, s);
+            prof_end(hc.mat, nh);
             prov_->release_head_chunk(ci);
         }
-        for (int i0 = 0; i0 < n; i0 += FTOK) {
-            const int nt = std::min(FTOK, n - i0);
-            const size_t toff = size_t(i0 / FTOK) * tile_stride;
-            head_argmax_final(hpv_.as<float>() + toff, hpi_.as<int>() + toff, head_blocks_,
-                              hpv_.as<float>() + toff + size_t(head_blocks_) * FTOK, i0, nt, amax_.as<uint32_t>(), s);
-        }
+        head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(), s);
     }
     prov_->end_forward();
     pos_ += t;
@@ -696,8 +764,9 @@ void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argm
         forward_chunk(tok + a, dtok + a, len, ci + 1 == n_chunks ? 1 : 0, logits != nullptr);
     }
     chunk_index_ = 0;
-    if (logits) HIPC(hipMemcpyAsync(logits, logits_.p, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
-    if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, 4, hipMemcpyDeviceToHost, stream_));
+    if (logits)
+        HIPC(hipMemcpyAsync(logits, logits_.as<float>() + head_off_ * vpad_, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
+    if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.as<uint32_t>() + head_off_, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
     if (argmax) *argmax = h_out_.as<uint32_t>()[0];
@@ -712,12 +781,21 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
     chunk_index_ = 0;
     forward_chunk(tok, stage_tokens(tok, n), n, n_logits, logits != nullptr);
     if (logits)
-        HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.p, vpad_ * 4, cfg_.vocab * 4, n_logits, hipMemcpyDeviceToHost,
-                              stream_));
-    if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.p, n_logits * 4, hipMemcpyDeviceToHost, stream_));
+        HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.as<float>() + head_off_ * vpad_, vpad_ * 4, cfg_.vocab * 4,
+                              n_logits, hipMemcpyDeviceToHost, stream_));
+    if (argmax)
+        HIPC(hipMemcpyAsync(h_out_.p, amax_.as<uint32_t>() + head_off_, n_logits * 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
     if (argmax) std::memcpy(argmax, h_out_.p, n_logits * 4);
+}
+
+void Model::verify_body(const uint32_t* block, size_t n) {
+    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
+    HIPC(hipMemcpyAsync(pos_dev_.p, h_pos_.p, 4, hipMemcpyHostToDevice, stream_));
+    forward_chunk(block, tok_.as<uint32_t>(), n, n, false);
+    accept_greedy(amax_.as<uint32_t>(), tok_.as<uint32_t>(), int(n), acc_.as<uint32_t>(), stream_);
+    HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
 }
 
 void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t* next) {
@@ -726,11 +804,34 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
     const size_t p = pos_;
     chunk_index_ = 0;
+    // Host staging; the previous call has drained, so the pinned buffers are free.
+    std::memcpy(h_tok_.p, block, n * 4);
+    h_pos_.as<int>()[0] = int(p);
     HIPC(hipEventRecord(ev0_, stream_));
-    const uint32_t* dtok = stage_tokens(block, n);
-    forward_chunk(block, dtok, n, n, false);
-    accept_greedy(amax_.as<uint32_t>(), dtok, int(n), acc_.as<uint32_t>(), stream_);
-    HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
+    if (graphs_on_ && !prof_ && prov_->resident()) {
+        auto it = graphs_.find(n);
+        if (it == graphs_.end()) {
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ge = nullptr;
+            HIPC(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            try {
+                verify_body(block, n);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream_, &g);
+                if (g) (void)hipGraphDestroy(g);
+                pos_ = p;
+                throw;
+            }
+            HIPC(hipStreamEndCapture(stream_, &g));
+            const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            HIPC(e);
+            it = graphs_.emplace(n, ge).first;
+        }
+        HIPC(hipGraphLaunch(it->second, stream_));
+    } else {
+        verify_body(block, n);
+    }
     HIPC(hipEventRecord(ev1_, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();

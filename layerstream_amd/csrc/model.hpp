@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <map>
 #include <memory>
 #include <vector>
 
@@ -83,8 +84,12 @@ public:
     virtual HeadChunk head_chunk(size_t c) = 0;
     virtual void release_head_chunk(size_t c) = 0;
     virtual void end_forward() = 0;
-    // x[t][h] = embedding rows of host tokens (device tokens copy for the resident table).
-    virtual void embed(const uint32_t* host_tokens, const uint32_t* dev_tokens, int t, float* x) = 0;
+    // True when every layer stays on the device (layer(l) may be asked for out of order).
+    virtual bool resident() const = 0;
+    // x[t][h] = embedding rows of host tokens (device tokens copy for the resident table); with
+    // frags also the fragments of x * w and the sum-of-squares partials.
+    virtual void embed(const uint32_t* host_tokens, const uint32_t* dev_tokens, int t, float* x, const float* w,
+                       uint8_t* frags, float* ss) = 0;
     virtual ls_report report() const = 0;
 };
 
@@ -108,6 +113,7 @@ public:
     double last_step_ms() const { return last_step_ms_; }
     int device() const { return device_; }
     void set_profiling(bool on);
+    void set_graphs(bool on);
     ls_kernel_stat read_profile();
 
 private:
@@ -116,9 +122,11 @@ private:
     // logits stored when want_logits.
     void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits);
     const uint32_t* stage_tokens(const uint32_t* tok, size_t n);
-    // B fragments of rows [i0, i0+nt) of x in global memory when they do not fit in LDS
-    // (nullptr: the kernel builds them in LDS).
-    const uint8_t* global_frags(const float* x, int i0, int nt, int cols, const float* w);
+    // The device part of a verify step (token and position copies from the pinned staging
+    // buffers, forward pass, acceptance, result copy): what a graph captures.
+    void verify_body(const uint32_t* block, size_t n);
+    void plan_kw_from_env();
+    int qkv_rg() const { return cfg_.head_dim > 64 ? int(cfg_.head_dim / 64) : 1; }
     void harvest();
     void prof_begin();
     void prof_end(const TMat& W, int nt);
@@ -129,13 +137,22 @@ private:
     hipStream_t stream_ = nullptr;
     std::unique_ptr<DeviceProvider> prov_;
     DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_, pos_dev_;
-    DevBuf x_, q_, attn_, act_frags_, in_frags_, head_frags_, attn_scratch_, logits_, hpv_, hpi_, amax_, tok_, acc_;
+    // x_: residual rows; xf_/ss_: fragments and sum-of-squares partials of the next normalised
+    // input; af_: attention output fragments; actf_: SiLU(g) * u fragments; part_/cnt_: split-K
+    // scratch; hpv_/hpi_: head-block argmax partials; row0_: logits of row 0.
+    DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, tok_, acc_;
+    int attn_splits_ = 1;
     PinnedBuf h_tok_, h_out_, h_pos_;
-    size_t vpad_ = 0, act_frag_bytes_ = 0;
-    int head_blocks_ = 0;
+    size_t vpad_ = 0, fb_h_ = 0, fb_q_ = 0, fb_in_ = 0;
+    int head_blocks_ = 0, slots_h_ = 0;
+    size_t head_off_ = 0;  // launch row of the first requested head row
+    // wavefronts along K per row group: q|k|v, o, gate|up, down, head
+    int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 4, kw_down_ = 8, kw_head_ = 7;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     bool prof_ = false;
+    bool graphs_on_ = true;
+    std::map<size_t, hipGraphExec_t> graphs_;  // verify step per block length
     std::vector<hipEvent_t> prof_ev_;
     size_t prof_used_ = 0;
     ls_kernel_stat prof_acc_{};

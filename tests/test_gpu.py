@@ -59,7 +59,8 @@ def test_matmul_matches_the_oracle_and_is_batch_invariant(f):
     rng = np.random.default_rng(1)
     pool = O.lib().or_pool_new(4)
     try:
-        for rows, cols in [(37, 128), (64, 256), (150, 192)]:
+        # the two wide shapes split K over 5 and 16 workgroups (last-arriver fixup)
+        for rows, cols in [(37, 128), (64, 256), (150, 192), (96, 4864), (40, 16384)]:
             if f[0] != 16 and cols % f[1]:
                 continue
             w = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
@@ -286,6 +287,38 @@ def test_verify_step_accepts_the_longest_matching_prefix():
         want_m = min(m_want, 5)
         assert acc == want_m and nxt == g[1 + want_m], (m_want, acc, nxt)
         assert tgt.pos() == len(PROMPT) + acc + 1
+
+
+def test_graph_replays_match_eager_steps_bit_for_bit():
+    """Verify steps replayed from captured HIP graphs (several block lengths, each replayed more
+    than once, with eager forward passes and synchronisations in between) against a model that
+    runs every step launch by launch."""
+    m = tiny("int8")
+    g = O.plain_greedy(cpu_model(m), PROMPT, 40)
+    eager, graph = gpu_model(m), gpu_model(m)
+    eager.use_graphs(False)
+    a_e, a_g = eager.forward_argmax(PROMPT), graph.forward_argmax(PROMPT)
+    assert a_e == a_g == g[0]
+    last, done = a_e, 1
+    for step, (k, good) in enumerate([(3, 1), (8, 2), (3, 0), (8, 5), (1, 0), (8, 8), (3, 3), (8, 1)]):
+        say("graph step", step, k, good)
+        drafts = list(g[done : done + good]) + [(g[done + good] + 7) % T.VOCAB] * (k - good)
+        drafts = drafts[:k]
+        r_e = eager.verify_greedy([last] + drafts)
+        r_g = graph.verify_greedy([last] + drafts)
+        assert r_e == r_g, (step, r_e, r_g)
+        assert eager.pos() == graph.pos()
+        acc, nxt = r_e
+        assert nxt == g[done + acc], (step, acc, nxt)
+        done += acc + 1
+        last = nxt
+        if step % 3 == 1:
+            # eager work on the graph model between replays: one token forward, then roll back
+            p = graph.pos()
+            le, lg = eager.forward([last]), graph.forward([last])
+            assert np.array_equal(bits(le), bits(lg)), step
+            eager.truncate(p)
+            graph.truncate(p)
 
 
 # ------------------------------------------------------------------------------ 0.5B shape
