@@ -124,6 +124,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=["resident", "stream"], default="resident")
+    ap.add_argument("--no-graphs", action="store_true", help="launch each kernel of a verify step separately (for tracers)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -151,6 +152,8 @@ def main():
     t0 = time.time()
     model = LS.Model(src, LS.MODE_STREAM if args.mode == "stream" else LS.MODE_RESIDENT, 2, max_ctx)
     log(f"model load {time.time() - t0:.1f}s")
+    if args.no_graphs:
+        model.use_graphs(False)
     # The drafter's script: the target's own greedy continuation.
     t0 = time.time()
     g = LS.greedy_generate(model, prompt, GREEDY_REF)
@@ -220,6 +223,7 @@ def main():
             "k": k,
             "ctx_start": ctx0,
             "ctx_mean": round(ctx_mean, 1),
+            "graphs": not args.no_graphs,
         },
         "verify_ms_p50": round(step_ms_p50, 4),
         "verify_ms_p90": round(float(np.percentile(tms, 90)), 4),

@@ -407,7 +407,7 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
         ls::DevBuf frags(ls::frag_tile_bytes(int(cols)) * tiles);
         HIPC(hipMemsetAsync(frags.p, 0, frags.n, s));
         ls::x_frags(x_dev, int(t), int(cols), nullptr, frags.as<uint8_t>(), nullptr, s);
-        const ls::MMPlan plan = ls::mm_plan(W, 1, 8, int(t));
+        const ls::MMPlan plan = ls::mm_plan(W, 1, 8, int(t), 1);
         ls::DevBuf part(std::max<size_t>(1, ls::mm_part_floats(plan)) * 4);
         ls::DevBuf cnt(std::max<size_t>(1, ls::mm_counters(plan)) * 4);
         HIPC(hipMemsetAsync(cnt.p, 0, cnt.n, s));

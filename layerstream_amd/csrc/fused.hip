@@ -71,14 +71,20 @@ __device__ __forceinline__ uint32_t raw_elem(const uint8_t* row, int bits, int g
 }
 
 // One thread per (row, chunk): the 64 bytes of its four lane slots.
-__global__ void k_tile_repack(const uint8_t* __restrict__ raw, int rows, TMat m, int row_off, int block, int stride) {
+__global__ void k_tile_repack(const uint8_t* __restrict__ raw, int rows, TMat m, int row_off, int block, int stride,
+                              int pair_hd) {
     const int r = blockIdx.x;
     if (r >= rows) return;
     const int bits = m.bits, K = m.cols;
     const int db = bits == 16 ? 2 * K : K * bits / 8;
     const int ng_real = bits == 16 ? 0 : K / m.group;
     const uint8_t* row = raw + size_t(r) * (db + 2 * ng_real);
-    const int dr = row_off + (r / block) * stride + r % block, strip = dr / 16, rl = dr % 16;
+    int lr = r;
+    if (pair_hd > 0) {
+        const int d = r % pair_hd, half = pair_hd / 2;
+        lr = r - d + (d < half ? 2 * d : 2 * (d - half) + 1);
+    }
+    const int dr = row_off + (lr / block) * stride + lr % block, strip = dr / 16, rl = dr % 16;
     const int cc = tile_chunk_cols(bits), Q = cc / 32;
     uint8_t* data = const_cast<uint8_t*>(m.data);
     for (int c = threadIdx.x; c < m.n_chunks; c += blockDim.x) {
@@ -111,18 +117,20 @@ __global__ void k_tile_repack(const uint8_t* __restrict__ raw, int rows, TMat m,
     }
 }
 
-void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int block, int stride, hipStream_t s) {
+void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int block, int stride, hipStream_t s,
+                 int pair_hd) {
     if (rows <= 0) return;
-    hipLaunchKernelGGL(k_tile_repack, dim3(rows), dim3(64), 0, s, raw, rows, dst, row_off, block, stride);
+    if (pair_hd > 0 && (pair_hd % 2 || rows % pair_hd)) throw std::runtime_error("RoPE pairing needs whole even heads");
+    hipLaunchKernelGGL(k_tile_repack, dim3(rows), dim3(64), 0, s, raw, rows, dst, row_off, block, stride, pair_hd);
     FCHECK(hipGetLastError());
 }
 
-// Sum of squares of 64 values v(0..63) in the one order used everywhere: eight sequential sums
-// of eight, added in order.
+// Sum of squares of 16 values v(0..15) (n of them, the rest zero) in the one order used
+// everywhere: two sequential sums of eight, added.
 template <class F>
-__device__ __forceinline__ float ss64(F v, int n) {
+__device__ __forceinline__ float ss16(F v, int n) {
     float s = 0.0f;
-    for (int b = 0; b < 8; b++) {
+    for (int b = 0; b < 2; b++) {
         float sb = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -135,7 +143,7 @@ __device__ __forceinline__ float ss64(F v, int n) {
     return s;
 }
 
-// Row i of x -> fragment slots of token i (x * w when w is set) and per-64-column sums of
+// Row i of x -> fragment slots of token i (x * w when w is set) and per-16-column sums of
 // squares. The row (cols values, a multiple of 8) is staged in LDS; one workgroup per token.
 __device__ void row_frags(const float* xr, int i, int cols, const float* __restrict__ w, uint8_t* frags, float* ss,
                           float* lds) {
@@ -153,8 +161,8 @@ __device__ void row_frags(const float* xr, int i, int cols, const float* __restr
     if (!ss) return;
     const int slots = ss_slots(cols);
     for (int g = threadIdx.x; g < slots; g += blockDim.x) {
-        const int n = min(64, cols - 64 * g);
-        ss[(size_t(tile) * slots + g) * FTOK + tok] = ss64([&](int c) { return lds[64 * g + c]; }, n);
+        const int n = min(16, cols - 16 * g);
+        ss[(size_t(tile) * slots + g) * FTOK + tok] = ss16([&](int c) { return lds[16 * g + c]; }, n);
     }
 }
 
@@ -260,17 +268,18 @@ struct Steps {
 };
 
 // Weights are read once per pass: non-temporal loads keep them from displacing the activations.
+template <int S>
 __device__ __forceinline__ void load_chunk(const uint8_t* base, size_t sstride, int c, uint4* raw) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
+    for (int r = 0; r < S; r++) {
         const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + r * sstride + size_t(c) * 1024));
         raw[r] = make_uint4(v[0], v[1], v[2], v[3]);
     }
 }
 
-// One chunk: Q k-steps x 4 strips x 3 MFMAs, with group scaling. B[q][term] are the fragments of
+// One chunk: Q k-steps x S strips x 3 MFMAs, with group scaling. B[q][term] are the fragments of
 // the chunk's k-steps; [ks_begin, ks_end) is the wavefront's k-step range.
-template <int BITS, bool G16>
+template <int BITS, bool G16, int S>
 __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_begin, int ks_end, const uint4 (*B)[3],
                                            const uint4* raw, f32x4* acc, f32x4* total) {
     const int lane = threadIdx.x & 63;
@@ -281,16 +290,16 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
         const int ks = c * Q + q;
         if constexpr (BITS == 16) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) total[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], total[r]);
+            for (int r = 0; r < S; r++) total[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], total[r]);
         } else if constexpr (!G16) {
             const bool first = (ks * 32) % G == 0 || ks == ks_begin;
             const bool last = ((ks + 1) * 32) % G == 0 || ks == ks_end - 1;
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], first ? f32x4{0, 0, 0, 0} : acc[r]);
+            for (int r = 0; r < S; r++) acc[r] = mfma3(a_operand<BITS>(raw[r], q), B[q], first ? f32x4{0, 0, 0, 0} : acc[r]);
             if (last) {
                 const int g = ks * 32 / G;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
+                for (int r = 0; r < S; r++) {
                     const f32x4 sc = scales4(W.scales, s0 + r, W.n_groups, g, lane);
 #pragma unroll
                     for (int i = 0; i < 4; i++) total[r][i] = __builtin_fmaf(sc[i], acc[r][i], total[r][i]);
@@ -300,7 +309,7 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
             // Groups of 16: lanes 0-31 hold the k-step's first group, lanes 32-63 the second.
             const bool lo = lane < 32;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
+            for (int r = 0; r < S; r++) {
                 const uint4 A = a_operand<BITS>(raw[r], q), Z = make_uint4(0, 0, 0, 0);
                 const f32x4 a1 = mfma3(lo ? A : Z, B[q], f32x4{0, 0, 0, 0});
                 const f32x4 a2 = mfma3(lo ? Z : A, B[q], f32x4{0, 0, 0, 0});
@@ -319,21 +328,22 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
 enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_HEAD = 3 };
 
 // 1 / rms per token of a tile from the producer's sum-of-squares partials, by one wavefront:
-// lane (part, token) adds slots part, part + 4, ... in order (every load issued first), then a
+// lane (part, token) adds slots part, part + 4, ... in order (loads issued 16 at a time), then a
 // fixed shuffle tree over the four parts (src/kernels.rs:217-228 up to the summation order).
-constexpr int SS_SLOTS_MAX = 64;
 __device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, float* inv) {
     const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
     const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
-    float x[SS_SLOTS_MAX / 4];
-#pragma unroll
-    for (int k = 0; k < SS_SLOTS_MAX / 4; k++) {
-        const int sl = part + 4 * k;
-        x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
-    }
     float v = 0.0f;
+    for (int k0 = 0; part + 4 * k0 < a.ss_slots; k0 += 16) {
+        float x[16];
 #pragma unroll
-    for (int k = 0; k < SS_SLOTS_MAX / 4; k++) v += x[k];
+        for (int k = 0; k < 16; k++) {
+            const int sl = part + 4 * (k0 + k);
+            x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) v += x[k];
+    }
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     if (lane < FTOK) inv[lane] = 1.0f / sqrtf(v / float(cols) + a.eps);
@@ -347,31 +357,39 @@ __device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
     return ia < ib;
 }
 
+// q|k rows are stored with each head's RoPE pairs adjacent: tile row 2j holds dimension j and
+// tile row 2j + 1 dimension j + hd / 2. Reference row of a tile row of the q|k|v matrix:
+__device__ __forceinline__ int qkv_ref_row(int row, int hd, int qk_rows) {
+    if (row >= qk_rows) return row;
+    const int r = row % hd;
+    return row - r + ((r & 1) ? hd / 2 + (r >> 1) : (r >> 1));
+}
+
 // Cache policy of the split-K pieces: sc1, coherent across the L2s of the XCDs.
 constexpr int CPOL_SC1 = 16;
 constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
 constexpr int MAX_SPLIT = 16;
 constexpr int ROPE_HALF_MAX = 128;
 
-// Dynamic LDS: [wavefront sums (kw > 1)] [tile: 64 rg rows x 16 floats] [16 inverse rms]
+// Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
 // [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
-// 64 rg x 16, per-row vector 64 rg, RoPE cos and sin 2 x 16 x half].
-template <int BITS, int EPI, bool G16>
-__global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+// 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half].
+template <int BITS, int EPI, bool G16, int S>
+__global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
     extern __shared__ __align__(16) uint8_t smem[];
     const int nw = p.rg * p.kw, nthr = nw * 64;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int tile = blockIdx.y, rb = blockIdx.x / p.nsplit, sp = blockIdx.x % p.nsplit;
-    const int rows_wg = 64 * p.rg, row0 = rb * rows_wg;
+    const int rows_wg = 16 * S * p.rg, row0 = rb * rows_wg;
     const int nt = min(FTOK, a.n - tile * FTOK);
     const TMat& W = a.W;
     const int rgi = wv / p.kw, kw = wv % p.kw;
-    const int s0 = (rb * p.rg + rgi) * 4;
+    const int s0 = (rb * p.rg + rgi) * S;
     const int c0 = (sp * p.kw + kw) * CPW;
     const int nch = min(CPW, W.n_chunks - c0);  // chunks of this wavefront (none when <= 0)
 
-    const size_t red_bytes = p.kw > 1 ? size_t(nw) * 4 * 64 * 16 : 0;
+    const size_t red_bytes = p.kw > 1 ? size_t(nw) * S * 64 * 16 : 0;
     float* tl = reinterpret_cast<float*>(smem + red_bytes);
     float* inv = tl + rows_wg * FTOK;
     int* flag = reinterpret_cast<int*>(inv + FTOK);
@@ -384,7 +402,7 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
 
     // Every load of the wavefront's share is issued before any arithmetic.
-    uint4 raw[CPW][4];
+    uint4 raw[CPW][S];
     uint4 B[CPW * Q][3];
     {
         const uint8_t* wb = W.data + (size_t(s0) * W.n_chunks * 64 + lane) * 16;
@@ -393,7 +411,7 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
 #pragma unroll
         for (int c = 0; c < CPW; c++) {
             if (c < nch) {
-                load_chunk(wb, sst, c0 + c, raw[c]);
+                load_chunk<S>(wb, sst, c0 + c, raw[c]);
 #pragma unroll
                 for (int q = 0; q < Q; q++) {
                     const int ks = (c0 + c) * Q + q;
@@ -404,6 +422,7 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
         }
     }
     // Epilogue operands, staged in LDS while the weights are in flight.
+    int pos0 = 0;
     if constexpr (EPI == EPI_RESID) {
         for (int e0 = threadIdx.x; e0 < rows_wg * FTOK; e0 += 4 * nthr) {
             float xv[4];
@@ -419,8 +438,11 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
         if (a.onorm)
             for (int r = threadIdx.x; r < rows_wg; r += nthr) vec[r] = row0 + r < W.rows ? a.onorm[row0 + r] : 0.0f;
     } else if constexpr (EPI == EPI_QKV) {
-        for (int r = threadIdx.x; r < rows_wg; r += nthr) vec[r] = row0 + r < W.rows ? a.bias[row0 + r] : 0.0f;
-        const int half = a.hd / 2, pos0 = *a.pos0;
+        const int qk = (a.heads + a.kv_heads) * a.hd;
+        for (int r = threadIdx.x; r < rows_wg; r += nthr)
+            vec[r] = row0 + r < W.rows ? a.bias[qkv_ref_row(row0 + r, a.hd, qk)] : 0.0f;
+        const int half = a.hd / 2;
+        pos0 = *a.pos0;
         for (int e = threadIdx.x; e < nt * half; e += nthr) {
             const int tok = e / half, j = e % half;
             const size_t at = size_t(pos0 + ibase + tok) * half + j;
@@ -428,38 +450,38 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
             rsin[tok * half + j] = a.rope_sin[at];
         }
     }
-    // 1 / rms per token from the producer's sum-of-squares partials (fixed order).
     if (a.ss && wv == 0) inv_rms(a, tile, W.cols, inv);
 
-    f32x4 total[4], acc[4];
+    f32x4 total[S], acc[S];
 #pragma unroll
-    for (int r = 0; r < 4; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
+    for (int r = 0; r < S; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < CPW; c++)
-        if (c < nch) chunk_mfma<BITS, G16>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
+        if (c < nch) chunk_mfma<BITS, G16, S>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
 
-    // Row-group tile: the kw wavefront sums added in wavefront order.
+    // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
+    // rows 16 r + 4 (l / 16) + i of token l % 16.
     if (p.kw > 1) {
         f32x4* red = reinterpret_cast<f32x4*>(smem);
 #pragma unroll
-        for (int r = 0; r < 4; r++) red[(wv * 4 + r) * 64 + lane] = total[r];
+        for (int r = 0; r < S; r++) red[(wv * S + r) * 64 + lane] = total[r];
         __syncthreads();
-        for (int e = threadIdx.x; e < p.rg * 256; e += nthr) {
-            const int g = e >> 8, r = (e >> 6) & 3, ln = e & 63;
-            f32x4 sum = red[((g * p.kw) * 4 + r) * 64 + ln];
+        for (int e = threadIdx.x; e < p.rg * S * 64; e += nthr) {
+            const int g = e / (S * 64), r = (e / 64) % S, ln = e % 64;
+            f32x4 sum = red[((g * p.kw) * S + r) * 64 + ln];
             for (int k = 1; k < p.kw; k++) {
-                const f32x4 v = red[((g * p.kw + k) * 4 + r) * 64 + ln];
+                const f32x4 v = red[((g * p.kw + k) * S + r) * 64 + ln];
 #pragma unroll
                 for (int i = 0; i < 4; i++) sum[i] += v[i];
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) tl[(64 * g + 16 * r + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
+            for (int i = 0; i < 4; i++) tl[(16 * (S * g + r) + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
         }
     } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++)
+        for (int r = 0; r < S; r++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) tl[(64 * rgi + 16 * r + 4 * (lane >> 4) + i) * FTOK + (lane & 15)] = total[r][i];
+            for (int i = 0; i < 4; i++) tl[(16 * (S * rgi + r) + 4 * (lane >> 4) + i) * FTOK + (lane & 15)] = total[r][i];
     }
     __syncthreads();
 
@@ -504,35 +526,30 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     }
 
     if constexpr (EPI == EPI_QKV) {
-        // rows: [0, h) q heads, [h, h + kv) k heads, [h + kv, h + 2 kv) v heads
+        // Tile rows: q heads, k heads (RoPE pairs adjacent), v heads (src/kernels.rs:242-252).
         const int hd = a.hd, half = hd / 2, h = a.heads * hd, kvd = a.kv_heads * hd;
-        const int pos0 = *a.pos0;
-        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
-            const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-            if (tok >= nt || row >= W.rows) continue;
-            const float v = a.ss ? __fmul_rn(tl[e], inv[tok]) : tl[e];
-            tl[e] = __fadd_rn(v, vec[rl]);
-        }
-        __syncthreads();
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
             if (tok >= nt || row >= W.rows) continue;
             const int i = ibase + tok, pos = pos0 + i;
-            float v = tl[e];
-            if (row < h + kvd) {  // RoPE, rotate half (src/kernels.rs:242-252)
-                const int d = row % hd, j = d % half;
+            const float iv = a.ss ? inv[tok] : 1.0f;
+            float v = __fadd_rn(a.ss ? __fmul_rn(tl[e], iv) : tl[e], vec[rl]);
+            int ref = row;
+            if (row < h + kvd) {
+                const int r = row % hd, j = r >> 1, pr = rl ^ 1;
+                const float pv = __fadd_rn(a.ss ? __fmul_rn(tl[pr * FTOK + tok], iv) : tl[pr * FTOK + tok], vec[pr]);
                 const float c = rcos[tok * half + j], sn = rsin[tok * half + j];
-                if (d < half) {
-                    const float b = tl[(rl + half) * FTOK + tok];
-                    v = __fsub_rn(__fmul_rn(v, c), __fmul_rn(b, sn));
+                if ((r & 1) == 0) {
+                    v = __fsub_rn(__fmul_rn(v, c), __fmul_rn(pv, sn));  // dimension j: x_j c - x_{j+half} s
+                    ref = row - r + j;
                 } else {
-                    const float aa = tl[(rl - half) * FTOK + tok];
-                    v = __fadd_rn(__fmul_rn(v, c), __fmul_rn(aa, sn));
+                    v = __fadd_rn(__fmul_rn(v, c), __fmul_rn(pv, sn));  // dimension j + half: x c + x_j s
+                    ref = row - r + half + j;
                 }
             }
-            if (row < h) a.out[size_t(i) * a.ldo + row] = v;
-            else if (row < h + kvd) a.kcache[size_t(pos) * kvd + (row - h)] = v;
-            else a.vcache[size_t(pos) * kvd + (row - h - kvd)] = v;
+            if (ref < h) a.out[size_t(i) * a.ldo + ref] = v;
+            else if (ref < h + kvd) a.kcache[size_t(pos) * kvd + (ref - h)] = v;
+            else a.vcache[size_t(pos) * kvd + (ref - h - kvd)] = v;
         }
     } else if constexpr (EPI == EPI_RESID) {
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
@@ -547,38 +564,35 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
         __syncthreads();
         if (a.ofrags) {
             uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
-            for (int sl = threadIdx.x; sl < (rows_wg / 32) * 64; sl += nthr) {
-                const int ksl = sl >> 6, ln = sl & 63, tok = ln & 15;
-                const int cl = 32 * ksl + 8 * (ln >> 4);
+            for (int q = threadIdx.x; q < (rows_wg / 8) * FTOK; q += nthr) {
+                const int cg = q / FTOK, tok = q % FTOK, col = row0 + 8 * cg;
                 float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const float x = tl[(cl + j) * FTOK + tok];
-                    v[j] = a.onorm ? __fmul_rn(x, vec[cl + j]) : x;
+                    const float x = tl[(8 * cg + j) * FTOK + tok];
+                    v[j] = a.onorm ? __fmul_rn(x, vec[8 * cg + j]) : x;
                 }
-                write_slot(tf, row0 / 32 + ksl, ln, v);
+                write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
             }
         }
         if (a.oss) {
-            for (int e = threadIdx.x; e < p.rg * FTOK; e += nthr) {
-                const int g = e / FTOK, tok = e % FTOK, slot = row0 / 64 + g;
+            for (int q = threadIdx.x; q < (rows_wg / 16) * FTOK; q += nthr) {
+                const int g = q / FTOK, tok = q % FTOK, slot = row0 / 16 + g;
                 if (slot >= a.oss_slots) continue;
-                a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] =
-                    ss64([&](int c) { return tl[(64 * g + c) * FTOK + tok]; }, 64);
+                a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] = ss16([&](int c) { return tl[(16 * g + c) * FTOK + tok]; }, 16);
             }
         }
     } else if constexpr (EPI == EPI_SILU) {
-        // rows: [64 gate rows | 64 up rows] for act columns 64 * rb + [0, 64)
+        // rows: [16 S gate rows | 16 S up rows] for act columns 16 S rb + [0, 16 S)
         uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
-        for (int sl = threadIdx.x; sl < 2 * 64; sl += nthr) {
-            const int ksl = sl >> 6, ln = sl & 63, tok = ln & 15;
-            const int cl = 32 * ksl + 8 * (ln >> 4);
+        for (int q = threadIdx.x; q < (2 * S) * FTOK; q += nthr) {
+            const int cg = q / FTOK, tok = q % FTOK, col = 16 * S * rb + 8 * cg;
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 v[j] = 0.0f;
                 if (tok < nt) {
-                    float g = tl[(cl + j) * FTOK + tok], up = tl[(64 + cl + j) * FTOK + tok];
+                    float g = tl[(8 * cg + j) * FTOK + tok], up = tl[(16 * S + 8 * cg + j) * FTOK + tok];
                     if (a.ss) {
                         g = __fmul_rn(g, inv[tok]);
                         up = __fmul_rn(up, inv[tok]);
@@ -586,7 +600,7 @@ __global__ __launch_bounds__(512) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
                     v[j] = __fmul_rn(g / (1.0f + expf(-g)), up);
                 }
             }
-            write_slot(tf, 2 * rb + ksl, ln, v);
+            write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
     } else {
         // Output head: logits, optional store, per-token best (value, index) of this block.
@@ -665,7 +679,7 @@ __global__ __launch_bounds__(64 * HEAD_WAVES) void k_head(MMArgs a, int n_groups
     uint4 raw[HEAD_PF][4];
 #pragma unroll
     for (int p = 0; p < HEAD_PF; p++)
-        if (p < F) load_chunk(wbase(p), sst, p % NC, raw[p]);
+        if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
 
     const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
     for (int i = threadIdx.x; i < nks * 3 * 64; i += blockDim.x) bl[i] = fb[i];
@@ -692,8 +706,8 @@ __global__ __launch_bounds__(64 * HEAD_WAVES) void k_head(MMArgs a, int n_groups
             for (int q = 0; q < Q; q++)
 #pragma unroll
                 for (int t = 0; t < 3; t++) B[q][t] = bl[((c * Q + q) * 3 + t) * 64 + lane];
-            chunk_mfma<BITS, G16>(W, 4 * g, c, 0, nks, B, raw[p], acc, total);
-            if (f + HEAD_PF < F) load_chunk(wbase(f + HEAD_PF), sst, (f + HEAD_PF) % NC, raw[p]);
+            chunk_mfma<BITS, G16, 4>(W, 4 * g, c, 0, nks, B, raw[p], acc, total);
+            if (f + HEAD_PF < F) load_chunk<4>(wbase(f + HEAD_PF), sst, (f + HEAD_PF) % NC, raw[p]);
             if (c == NC - 1) {
                 // Group done: logits, optional store, argmax over its 64 rows per token.
                 const int tok = lane & 15;
@@ -768,73 +782,77 @@ int device_cu_count() {
 
 constexpr size_t HEAD_LDS_MAX = 150 * 1024;
 
-MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens) {
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
     MMPlan p;
+    if (strips != 1 && strips != 2 && strips != 4) throw std::runtime_error("1, 2 or 4 strips per wavefront");
+    p.s = strips;
     p.rg = rg;
     p.kw = kw < 1 ? 1 : kw;
+    const int max_waves = strips == 4 ? 8 : 16;
     const int cpw = 4 / (W.bits == 16 ? 1 : (W.bits == 8 ? 2 : 4));
     const int waves_k = (W.n_chunks + cpw - 1) / cpw;  // wavefront shares along K
     if (p.kw > waves_k) p.kw = waves_k;
-    if (p.rg > 8) throw std::runtime_error("a matrix workgroup holds at most 8 wavefronts");
-    if (p.rg * p.kw > 8) p.kw = 8 / p.rg;
+    if (p.rg > max_waves) throw std::runtime_error("too many row groups for one workgroup");
+    if (p.rg * p.kw > max_waves) p.kw = max_waves / p.rg;
     p.nsplit = (waves_k + p.kw - 1) / p.kw;
-    while (p.nsplit > MAX_SPLIT && p.rg * (p.kw + 1) <= 8) {
+    while (p.nsplit > MAX_SPLIT && p.rg * (p.kw + 1) <= max_waves) {
         p.kw++;
         p.nsplit = (waves_k + p.kw - 1) / p.kw;
     }
     if (p.nsplit > MAX_SPLIT) throw std::runtime_error("matrix too wide for the split-K limit");
-    const int groups = W.n_strips / 4;
-    if (groups % rg) throw std::runtime_error("matrix rows do not fill whole row blocks");
-    p.nrb = groups / rg;
+    if (W.n_strips % (strips * rg)) throw std::runtime_error("matrix rows do not fill whole row blocks");
+    p.nrb = W.n_strips / (strips * rg);
     p.tiles = (n_tokens + FTOK - 1) / FTOK;
     return p;
 }
 
 size_t mm_part_floats(const MMPlan& p) {
-    return p.nsplit > 1 ? size_t(p.tiles) * p.nrb * p.nsplit * 64 * p.rg * FTOK : 0;
+    return p.nsplit > 1 ? size_t(p.tiles) * p.nrb * p.nsplit * 16 * p.s * p.rg * FTOK : 0;
 }
 size_t mm_counters(const MMPlan& p) { return p.nsplit > 1 ? size_t(p.tiles) * p.nrb : 0; }
 
 static size_t lds_bytes(const MMPlan& p) {
-    const size_t red = p.kw > 1 ? size_t(p.rg) * p.kw * 4 * 64 * 16 : 0;
-    const size_t rows = size_t(64 * p.rg);
+    const size_t red = p.kw > 1 ? size_t(p.rg) * p.kw * p.s * 64 * 16 : 0;
+    const size_t rows = size_t(16 * p.s * p.rg);
     return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX) * 4;
 }
 
-template <int EPI>
+template <int EPI, int S>
 static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    if (p.s != S) throw std::runtime_error("matrix plan does not match the kernel's strips per wavefront");
     if (p.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
     const dim3 grid(p.nrb * p.nsplit, p.tiles), block(64 * p.rg * p.kw);
     const size_t lds = lds_bytes(p);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
     switch (a.W.bits) {
-        case 16: hipLaunchKernelGGL((k_mm<16, EPI, false>), grid, block, lds, s, a, p, sc); break;
+        case 16: hipLaunchKernelGGL((k_mm<16, EPI, false, S>), grid, block, lds, s, a, p, sc); break;
         case 8:
-            if (g16) hipLaunchKernelGGL((k_mm<8, EPI, true>), grid, block, lds, s, a, p, sc);
-            else hipLaunchKernelGGL((k_mm<8, EPI, false>), grid, block, lds, s, a, p, sc);
+            if (g16) hipLaunchKernelGGL((k_mm<8, EPI, true, S>), grid, block, lds, s, a, p, sc);
+            else hipLaunchKernelGGL((k_mm<8, EPI, false, S>), grid, block, lds, s, a, p, sc);
             break;
         default:
-            if (g16) hipLaunchKernelGGL((k_mm<4, EPI, true>), grid, block, lds, s, a, p, sc);
-            else hipLaunchKernelGGL((k_mm<4, EPI, false>), grid, block, lds, s, a, p, sc);
+            if (g16) hipLaunchKernelGGL((k_mm<4, EPI, true, S>), grid, block, lds, s, a, p, sc);
+            else hipLaunchKernelGGL((k_mm<4, EPI, false, S>), grid, block, lds, s, a, p, sc);
             break;
     }
     FCHECK(hipGetLastError());
 }
 
 void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
-    if (64 * p.rg % a.hd) throw std::runtime_error("q/k/v row blocks must hold whole heads");
-    if (a.hd / 2 > ROPE_HALF_MAX) throw std::runtime_error("head_dim too large");
-    launch<EPI_QKV>(a, p, sc, s);
+    if (a.hd % 2 || a.hd / 2 > ROPE_HALF_MAX) throw std::runtime_error("head_dim must be even and at most 256");
+    if ((a.heads + a.kv_heads) * a.hd % 16) throw std::runtime_error("q|k rows must fill whole strips");
+    launch<EPI_QKV, 1>(a, p, sc, s);
 }
-void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) { launch<EPI_RESID>(a, p, sc, s); }
+void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) { launch<EPI_RESID, 1>(a, p, sc, s); }
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
-    if (p.rg != 2) throw std::runtime_error("gate|up runs in 128-row blocks");
-    launch<EPI_SILU>(a, p, sc, s);
+    if (p.rg != 2) throw std::runtime_error("gate|up runs gate and up row blocks together");
+    launch<EPI_SILU, GU_STRIPS>(a, p, sc, s);
 }
+
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES * FTOK * 8;
-    if (p.rg != 1 || lds > HEAD_LDS_MAX) {
-        launch<EPI_HEAD>(a, p, sc, s);
+    if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX) {
+        launch<EPI_HEAD, 4>(a, p, sc, s);
         return p.nrb;
     }
     // One workgroup of HEAD_WAVES wavefronts per CU (the fragments fill most of its LDS).

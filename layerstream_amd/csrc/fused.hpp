@@ -13,7 +13,7 @@
 // form by the kernel that produces it (embedding, attention, the residual and SiLU epilogues), so
 // the matrix kernels start streaming weights at once. Inputs that the reference RMS-normalises
 // are stored as x * w; the per-token 1 / rms is applied to the matrix output in the epilogue,
-// from sum-of-squares partials (one per 64 columns, [tile][slot][16 tokens]) that the producer
+// from sum-of-squares partials (one per 16 columns, [tile][slot][16 tokens]) that the producer
 // writes beside the fragments.
 #pragma once
 
@@ -44,15 +44,20 @@ size_t tile_data_bytes(const TMat& m);
 size_t tile_scale_bytes(const TMat& m);
 TMat tile_bind(const TMat& shape, uint8_t* data, uint16_t* scales);
 // Rearrange `rows` reference rows (raw, on the device) into the tile layout. Source row r goes
-// to destination row row_off + (r / block) * stride + r % block (block = rows: contiguous).
-void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int block, int stride, hipStream_t s);
+// to destination row row_off + (r / block) * stride + r % block (block = rows: contiguous); with
+// pair_hd > 0 the rows of each pair_hd-row head are first reordered so that RoPE pairs are
+// adjacent (row j -> 2j, row j + pair_hd / 2 -> 2j + 1).
+void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int block, int stride, hipStream_t s,
+                 int pair_hd = 0);
 // Initialise padding: zero-weight bytes and zero scales over the whole matrix.
 void tile_clear(const TMat& m, hipStream_t s);
 
 // Bytes of one token tile of fragments for `cols` input columns.
 __host__ __device__ inline size_t frag_tile_bytes(int cols) { return size_t(tile_kpad(cols)) / 32 * 3 * 1024; }
-// Sum-of-squares slots (64 columns each) of a row of `cols` values.
-__host__ __device__ inline int ss_slots(int cols) { return (cols + 63) / 64; }
+// Sum-of-squares slots (16 columns each) of a row of `cols` values.
+__host__ __device__ inline int ss_slots(int cols) { return (cols + 15) / 16; }
+// gate|up rows are interleaved in blocks of 16 * GU_STRIPS (gate block, up block, ...).
+constexpr int GU_STRIPS = 2;
 
 // Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization) into
 // x [n][cols], plus fragments of x * w and sum-of-squares partials.
@@ -95,14 +100,14 @@ struct MMArgs {
     float* row0 = nullptr;  // logits of row 0 per token ([tile * 16 + token]), when set
 };
 
-// Work split of one launch: each workgroup owns rg groups of 64 rows and one of nsplit K ranges,
-// cut among kw wavefronts per row group. With nsplit > 1 the pieces meet in `part` and the last
-// workgroup of a row block to finish adds them in split order (counters in `cnt` start at zero
-// and are left at zero).
+// Work split of one launch: each wavefront streams s strips (16 s rows); a workgroup owns rg
+// such row groups and one of nsplit K ranges, cut among kw wavefronts per row group. With
+// nsplit > 1 the pieces meet in `part` and the last workgroup of a row block to finish adds them
+// in split order (counters in `cnt` start at zero and are left at zero).
 struct MMPlan {
-    int rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
+    int s = 1, rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
 };
-MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens);
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips);
 size_t mm_part_floats(const MMPlan& p);
 size_t mm_counters(const MMPlan& p);
 
@@ -114,15 +119,18 @@ struct MMScratch {
     int* cnt = nullptr;
 };
 
-// QKV projection + 1/rms + bias + RoPE + K/V append. Rows: q heads, k heads, v heads.
+// QKV projection + 1/rms + bias + RoPE + K/V append (plan strips 1). Rows: q heads and k heads
+// with each head's RoPE pairs adjacent (tile row 2j: dimension j, 2j + 1: dimension j + hd / 2),
+// then v heads.
 void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
-// x[row] += W x; then fragments of x * onorm and sum-of-squares partials of the new rows.
+// x[row] += W x; then fragments of x * onorm and sum-of-squares partials of the new rows (plan
+// strips 1).
 void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
-// gate|up projection (row blocks of 64 interleaved gate, up; plan.rg == 2) + 1/rms +
-// SiLU(g) * u -> act fragments.
+// gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan strips GU_STRIPS,
+// rg 2) + 1/rms + SiLU(g) * u -> act fragments.
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
-// Output head: logits (1/rms applied), optional logits store, argmax partials at
-// [tile][arg_off + b][16] for b below the returned count.
+// Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
+// partials at [tile][arg_off + b][16] for b below the returned count.
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // Final argmax over head-block partials (src/spec.rs:41-49 rule) for n tokens; row0 holds
 // logits[.][0].

@@ -1,17 +1,18 @@
 // The device Model (src/model.rs) and its providers (src/provider.rs) on one MI355X.
 //
-// HBM layout: per layer one arena holding the fused q|k|v matrix, o, the fused gate|up matrix
-// (64-row blocks of gate and up interleaved) and down in the tile layout (fused.hpp), then the
-// q|k|v bias and the two RMSNorm weight vectors as f32. The tied embedding table is one
-// tile-layout matrix used both for the embedding gather and as the output head. The KV cache is
-// f32 [layer][max_ctx][kv_dim] for K and for V, as the reference's (src/model.rs:67-68);
-// rollback is O(1) (only `pos` moves).
+// HBM layout: per layer one arena holding the fused q|k|v matrix (q and k rows with each head's
+// RoPE pairs adjacent), o, the fused gate|up matrix (32-row blocks of gate and up interleaved)
+// and down in the tile layout (fused.hpp), then the q|k|v bias and the two RMSNorm weight
+// vectors as f32. The tied embedding table is one tile-layout matrix used both for the
+// embedding gather and as the output head. The KV cache is f32 [layer][max_ctx][kv_dim] for K
+// and for V, as the reference's (src/model.rs:67-68); rollback is O(1) (only `pos` moves).
 //
-// A forward pass over t tokens runs per layer: fused QKV (RMSNorm prologue, bias + RoPE + K/V
-// append epilogue), chunked attention and its combine, fused O projection (+ residual), fused
-// gate|up (RMSNorm prologue, SiLU(g) * u epilogue into B fragments) and fused down (+ residual),
-// each launched once per tile of 16 tokens; then the head (final RMSNorm prologue, per-block
-// argmax epilogue) and the argmax reduction.
+// A forward pass over t tokens (every 16-token tile in each launch) runs per layer: QKV (1/rms,
+// bias, RoPE and K/V append in the epilogue), attention (chunks and their combine in one
+// launch), O projection (+ residual, then the fragments of x * post_norm), gate|up (1/rms and
+// SiLU(g) * u into fragments) and down (+ residual, then the fragments of x * the next norm);
+// then the head (persistent, argmax partials) and the argmax reduction. Every kernel reads its
+// input as fragments written by the one before; the verify step is replayed from a HIP graph.
 #include "model.hpp"
 
 #include <chrono>
@@ -115,12 +116,13 @@ void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* ra
                         hipStream_t s) {
     const int h = int(c.hidden), kv = int(c.kv_dim()), in = int(c.inter);
     const DevLayer D = bind_layer(a, b);
-    tile_repack(raw + L.off[T_Q_W], h, D.qkv, 0, h, h, s);
-    tile_repack(raw + L.off[T_K_W], kv, D.qkv, h, kv, kv, s);
+    const int hd = int(c.head_dim), gb = 16 * GU_STRIPS;
+    tile_repack(raw + L.off[T_Q_W], h, D.qkv, 0, h, h, s, hd);
+    tile_repack(raw + L.off[T_K_W], kv, D.qkv, h, kv, kv, s, hd);
     tile_repack(raw + L.off[T_V_W], kv, D.qkv, h + kv, kv, kv, s);
     tile_repack(raw + L.off[T_O_W], h, D.o, 0, h, h, s);
-    tile_repack(raw + L.off[T_GATE], in, D.gu, 0, 64, 128, s);
-    tile_repack(raw + L.off[T_UP], in, D.gu, 64, 64, 128, s);
+    tile_repack(raw + L.off[T_GATE], in, D.gu, 0, gb, 2 * gb, s);
+    tile_repack(raw + L.off[T_UP], in, D.gu, gb, gb, 2 * gb, s);
     tile_repack(raw + L.off[T_DOWN], h, D.down, 0, h, h, s);
     float* bq = reinterpret_cast<float*>(b + a.b_qkv);
     bf16_to_f32_dev(raw + L.off[T_Q_B], h, bq, s);
@@ -457,6 +459,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     fb_in_ = frag_tile_bytes(int(in));
     slots_h_ = ss_slots(int(h));
     if (h > 4096) fail("hidden sizes above 4096 are not supported");
+    if ((c.heads + c.kv_heads) * c.head_dim % 16) fail("q and k heads must fill whole 16-row strips");
     {
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const size_t n_chunks = (c.vocab + HEAD_ROWS - 1) / HEAD_ROWS;
@@ -480,9 +483,9 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const int n = int(T);
         const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(HEAD_ROWS), int(h), 256);
-        const MMPlan plans[] = {mm_plan(la.qkv, qkv_rg(), kw_qkv_, n), mm_plan(la.o, 1, kw_o_, n),
-                                mm_plan(la.gu, 2, kw_gu_, n),           mm_plan(la.down, 1, kw_down_, n),
-                                mm_plan(e_res, 1, kw_head_, n),         mm_plan(e_chunk, 1, kw_head_, n)};
+        const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1),        mm_plan(la.o, 1, kw_o_, n, 1),
+                                mm_plan(la.gu, 2, kw_gu_, n, GU_STRIPS), mm_plan(la.down, 1, kw_down_, n, 1),
+                                mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};
         size_t pf = 0, nc = 0;
         for (const MMPlan& pl : plans) {
             pf = std::max(pf, mm_part_floats(pl));
@@ -592,7 +595,7 @@ void Model::plan_kw_from_env() {
     int v[5];
     if (std::sscanf(e, "%d,%d,%d,%d,%d", &v[0], &v[1], &v[2], &v[3], &v[4]) != 5) fail("LS_MM_KW needs five integers");
     for (int x : v)
-        if (x < 1 || x > 8) fail("LS_MM_KW values must be between 1 and 8");
+        if (x < 1 || x > 16) fail("LS_MM_KW values must be between 1 and 16");
     kw_qkv_ = v[0];
     kw_o_ = v[1];
     kw_gu_ = v[2];
@@ -656,7 +659,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.kv_heads = kvh;
             a.hd = hd;
             prof_begin();
-            mm_qkv(a, mm_plan(L.qkv, qkv_rg(), kw_qkv_, T), scr, s);
+            mm_qkv(a, mm_plan(L.qkv, 1, kw_qkv_, T, 1), scr, s);
             prof_end(L.qkv, T);
         }
         attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, int(max_ctx_), kc, vc, attn_scratch_.as<float>(), attn_cnt_.as<int>(),
@@ -675,7 +678,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.oss = ss;
             a.oss_slots = slots_h_;
             prof_begin();
-            mm_residual(a, mm_plan(L.o, 1, kw_o_, T), scr, s);
+            mm_residual(a, mm_plan(L.o, 1, kw_o_, T, 1), scr, s);
             prof_end(L.o, T);
         }
         {
@@ -690,7 +693,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.ofrags = actf_.as<uint8_t>();
             a.ofrag_stride = fb_in_;
             prof_begin();
-            mm_gate_up(a, mm_plan(L.gu, 2, kw_gu_, T), scr, s);
+            mm_gate_up(a, mm_plan(L.gu, 2, kw_gu_, T, GU_STRIPS), scr, s);
             prof_end(L.gu, T);
         }
         {
@@ -710,7 +713,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 a.oss_slots = slots_h_;
             }
             prof_begin();
-            mm_residual(a, mm_plan(L.down, 1, kw_down_, T), scr, s);
+            mm_residual(a, mm_plan(L.down, 1, kw_down_, T, 1), scr, s);
             prof_end(L.down, T);
         }
         prov_->release_layer(l);
@@ -740,7 +743,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.arg_off = blocks;
             a.row_base = int(hc.first);
             a.row0 = hc.first == 0 ? row0_.as<float>() : nullptr;
-            const MMPlan plan = mm_plan(hc.mat, 1, kw_head_, nh);
+            const MMPlan plan = mm_plan(hc.mat, 1, kw_head_, nh, 4);
             if (a.arg_off + plan.nrb > head_blocks_) fail("head blocks exceed the argmax buffer", LS_E_STATE);
             prof_begin();
             blocks += mm_head(a, plan, scr, s);

@@ -45,8 +45,9 @@ struct PinnedBuf {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
-// One transformer layer on the device, tile layout: q|k|v fused (rows h, kv, kv), gate|up fused
-// with 64-row blocks interleaved (gate block a, up block a, ...), o and down; f32 bias and norms.
+// One transformer layer on the device, tile layout: q|k|v fused (rows h, kv, kv; q and k rows
+// with RoPE pairs adjacent), gate|up fused with 16 GU_STRIPS-row blocks interleaved (gate block
+// a, up block a, ...), o and down; f32 bias and norms.
 struct DevLayer {
     TMat qkv, o, gu, down;
     const float* b_qkv = nullptr;
@@ -126,7 +127,6 @@ private:
     // buffers, forward pass, acceptance, result copy): what a graph captures.
     void verify_body(const uint32_t* block, size_t n);
     void plan_kw_from_env();
-    int qkv_rg() const { return cfg_.head_dim > 64 ? int(cfg_.head_dim / 64) : 1; }
     void harvest();
     void prof_begin();
     void prof_end(const TMat& W, int nt);
@@ -147,7 +147,7 @@ private:
     int head_blocks_ = 0, slots_h_ = 0;
     size_t head_off_ = 0;  // launch row of the first requested head row
     // wavefronts along K per row group: q|k|v, o, gate|up, down, head
-    int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 4, kw_down_ = 8, kw_head_ = 7;
+    int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 8, kw_head_ = 7;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     bool prof_ = false;
