@@ -9,6 +9,8 @@ A step is one fused verify pass (forward over k+1 rows, argmax, acceptance, roll
 steps, then exactly K timed steps. value = verified tokens (m+1 per step) / wall time.
 
 Usage: python bench.py [--gpus 1] [--steps 96] [--warmup 4] [--cpu-steps 24] [--no-cpu]
+       python bench.py --calibrate-copy MIB   (one device-to-device copy of MIB MiB, repeated: the
+                                               known-size kernel that scales HBM counter readings)
 """
 from __future__ import annotations
 
@@ -34,6 +36,39 @@ def hip_sync():
     h = C.CDLL("libamdhip64.so")
     if h.hipDeviceSynchronize() != 0:
         raise RuntimeError("hipDeviceSynchronize failed")
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mm_qwen05b_int8_verify_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per matrix launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE runs of this workload, scaled by a copy of known size), or None."""
+    import re
+
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def calibrate_copy(mib, reps=8):
+    """Plain device-to-device copies of a known size, for scaling FETCH_SIZE / WRITE_SIZE."""
+    h = C.CDLL("libamdhip64.so")
+    n = mib << 20
+    a, b = C.c_void_p(), C.c_void_p()
+    if h.hipMalloc(C.byref(a), C.c_size_t(n)) or h.hipMalloc(C.byref(b), C.c_size_t(n)):
+        raise RuntimeError("hipMalloc failed")
+    h.hipMemset(a, 1, C.c_size_t(n))
+    for _ in range(reps):
+        if h.hipMemcpy(b, a, C.c_size_t(n), 3):  # hipMemcpyDeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+    hip_sync()
+    h.hipFree(a)
+    h.hipFree(b)
+    print(json.dumps({"calibration": "device-to-device copy", "bytes_read": n, "bytes_written": n, "reps": reps}), flush=True)
 
 
 def log(*a):
@@ -125,12 +160,18 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=["resident", "stream"], default="resident")
     ap.add_argument("--no-graphs", action="store_true", help="launch each kernel of a verify step separately (for tracers)")
+    ap.add_argument("--greedy-ref", type=int, default=GREEDY_REF, help="tokens of greedy continuation scripting the drafter")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
 
     import layerstream_amd as LS
 
@@ -145,7 +186,7 @@ def main():
     row_bytes = LS.row_bytes(cfg["embed_format"], cfg["hidden"])
     k, W, K = args.k, args.warmup, args.steps
     max_new = 9 * (W + K + ROOF_STEPS) + 2
-    max_ctx = args.ctx + max(max_new, GREEDY_REF) + k + 8
+    max_ctx = args.ctx + max(max_new, args.greedy_ref) + k + 8
     rng = np.random.default_rng(512)
     prompt = rng.integers(0, cfg["vocab"], args.ctx).tolist()
 
@@ -156,7 +197,7 @@ def main():
         model.use_graphs(False)
     # The drafter's script: the target's own greedy continuation.
     t0 = time.time()
-    g = LS.greedy_generate(model, prompt, GREEDY_REF)
+    g = LS.greedy_generate(model, prompt, args.greedy_ref) if args.greedy_ref > 0 else []
     model.reset()
     log(f"greedy reference {len(g)} tokens in {time.time() - t0:.1f}s")
     seed = 2024
@@ -197,9 +238,10 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(),
+        "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
         "kernel": "k_mm (fused MFMA weight-streaming matmul: q|k|v, o, gate|up, down, head; int8, t=9)",
-        "measured_over": f"{ROOF_STEPS} verify steps after the timed ones, HIP events around each launch",
+        "measured_over": f"{ROOF_STEPS} verify steps after the timed ones, start/stop events recorded by each dispatch (hipExtLaunchKernel)",
         "launches": int(prof["launches"]),
         "avg_launch_us": round(avg_ms * 1e3, 3),
         "avg_bytes_per_launch": round(avg_bytes),

@@ -13,6 +13,8 @@
 #include "fused.hpp"
 #include "frag_dev.hpp"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <cmath>
 #include <stdexcept>
@@ -653,13 +655,18 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
 // once; its wavefronts then stream 64-row groups of the table over the whole K range, PF chunks
 // ahead, and reduce each group to logits and a per-token (value, index) argmax partial inside
 // the wavefront (lane l holds rows 16 r + 4 (l / 16) + i of token l % 16).
-constexpr int HEAD_WAVES = 8;
 // Chunks in flight per wavefront (int4 chunks carry four k-steps of fragments each).
 template <int BITS, bool G16>
 constexpr int head_pf() { return BITS == 4 ? (G16 ? 1 : 2) : 3; }
+// Wavefronts per workgroup: 10 give 2560 on 256 CUs, so a 151936-row table (2374 groups of 64)
+// takes at most one group per wavefront; the groups-of-16 variants keep 8 for registers.
+template <bool G16>
+constexpr int head_waves() { return G16 ? 8 : 10; }
+constexpr int HEAD_WAVES_MAX = 10;
 
 template <int BITS, bool G16>
-__global__ __launch_bounds__(64 * HEAD_WAVES) void k_head(MMArgs a, int n_groups) {
+__global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n_groups) {
+    constexpr int HEAD_WAVES = head_waves<G16>();
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int Q = Steps<BITS>::Q, HEAD_PF = head_pf<BITS, G16>();
     const TMat& W = a.W;
@@ -682,7 +689,16 @@ __global__ __launch_bounds__(64 * HEAD_WAVES) void k_head(MMArgs a, int n_groups
         if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
 
     const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
-    for (int i = threadIdx.x; i < nks * 3 * 64; i += blockDim.x) bl[i] = fb[i];
+    const int nb = nks * 3 * 64, nthr = 64 * HEAD_WAVES;
+    for (int i0 = threadIdx.x; i0 < nb; i0 += 8 * nthr) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * nthr < nb) v[u] = fb[i0 + u * nthr];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * nthr < nb) bl[i0 + u * nthr] = v[u];
+    }
     if (wv == 0) {
         if (a.ss) inv_rms(a, tile, W.cols, inv);
         else if (lane < FTOK) inv[lane] = 1.0f;
@@ -817,6 +833,24 @@ static size_t lds_bytes(const MMPlan& p) {
     return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX) * 4;
 }
 
+static thread_local hipEvent_t t_start = nullptr, t_stop = nullptr;
+
+void mm_time_next_launch(hipEvent_t start, hipEvent_t stop) {
+    t_start = start;
+    t_stop = stop;
+}
+
+// hipLaunchKernelGGL, or the timed launch when events are pending.
+template <class K, class... Args>
+static void go(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+    if (t_start) {
+        hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), s, t_start, t_stop, 0u, args...);
+        t_start = t_stop = nullptr;
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+    }
+}
+
 template <int EPI, int S>
 static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     if (p.s != S) throw std::runtime_error("matrix plan does not match the kernel's strips per wavefront");
@@ -825,14 +859,14 @@ static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStr
     const size_t lds = lds_bytes(p);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
     switch (a.W.bits) {
-        case 16: hipLaunchKernelGGL((k_mm<16, EPI, false, S>), grid, block, lds, s, a, p, sc); break;
+        case 16: go(k_mm<16, EPI, false, S>, grid, block, lds, s, a, p, sc); break;
         case 8:
-            if (g16) hipLaunchKernelGGL((k_mm<8, EPI, true, S>), grid, block, lds, s, a, p, sc);
-            else hipLaunchKernelGGL((k_mm<8, EPI, false, S>), grid, block, lds, s, a, p, sc);
+            if (g16) go(k_mm<8, EPI, true, S>, grid, block, lds, s, a, p, sc);
+            else go(k_mm<8, EPI, false, S>, grid, block, lds, s, a, p, sc);
             break;
         default:
-            if (g16) hipLaunchKernelGGL((k_mm<4, EPI, true, S>), grid, block, lds, s, a, p, sc);
-            else hipLaunchKernelGGL((k_mm<4, EPI, false, S>), grid, block, lds, s, a, p, sc);
+            if (g16) go(k_mm<4, EPI, true, S>, grid, block, lds, s, a, p, sc);
+            else go(k_mm<4, EPI, false, S>, grid, block, lds, s, a, p, sc);
             break;
     }
     FCHECK(hipGetLastError());
@@ -850,25 +884,26 @@ void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream
 }
 
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
-    const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES * FTOK * 8;
+    const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES_MAX * FTOK * 8;
     if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX) {
         launch<EPI_HEAD, 4>(a, p, sc, s);
         return p.nrb;
     }
-    // One workgroup of HEAD_WAVES wavefronts per CU (the fragments fill most of its LDS).
+    // One workgroup per CU (the fragments fill most of its LDS).
     const int n_groups = p.nrb;
-    const int blocks = std::min(device_cu_count(), (n_groups + HEAD_WAVES - 1) / HEAD_WAVES);
-    const dim3 grid(blocks, p.tiles), block(64 * HEAD_WAVES);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
+    const int waves = g16 ? head_waves<true>() : head_waves<false>();
+    const int blocks = std::min(device_cu_count(), (n_groups + waves - 1) / waves);
+    const dim3 grid(blocks, p.tiles), block(64 * waves);
     switch (a.W.bits) {
-        case 16: hipLaunchKernelGGL((k_head<16, false>), grid, block, lds, s, a, n_groups); break;
+        case 16: go(k_head<16, false>, grid, block, lds, s, a, n_groups); break;
         case 8:
-            if (g16) hipLaunchKernelGGL((k_head<8, true>), grid, block, lds, s, a, n_groups);
-            else hipLaunchKernelGGL((k_head<8, false>), grid, block, lds, s, a, n_groups);
+            if (g16) go(k_head<8, true>, grid, block, lds, s, a, n_groups);
+            else go(k_head<8, false>, grid, block, lds, s, a, n_groups);
             break;
         default:
-            if (g16) hipLaunchKernelGGL((k_head<4, true>), grid, block, lds, s, a, n_groups);
-            else hipLaunchKernelGGL((k_head<4, false>), grid, block, lds, s, a, n_groups);
+            if (g16) go(k_head<4, true>, grid, block, lds, s, a, n_groups);
+            else go(k_head<4, false>, grid, block, lds, s, a, n_groups);
             break;
     }
     FCHECK(hipGetLastError());

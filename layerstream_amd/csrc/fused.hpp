@@ -113,6 +113,9 @@ size_t mm_counters(const MMPlan& p);
 
 // Compute units of the current device (cached after the first call).
 int device_cu_count();
+// Time the next matrix launch of this thread: the dispatch itself records `start` when the
+// kernel begins and `stop` when it ends (hipExtLaunchKernel), so no marker sits in between.
+void mm_time_next_launch(hipEvent_t start, hipEvent_t stop);
 
 struct MMScratch {
     float* part = nullptr;

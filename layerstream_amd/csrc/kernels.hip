@@ -139,7 +139,8 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
             }
         }
         __syncthreads();
-        // Scores: thread (row, sub) owns keys 4 sub .. 4 sub + 3; each dot product runs over d in order.
+        // Scores: thread (row, sub) owns keys sub + 16 u (rows 68 floats apart: the 16 lanes of a
+        // row read distinct banks); each dot product runs over d in order.
         float sc[4];
         {
             float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
                     const float4 q4 = *reinterpret_cast<const float4*>(Qs + row * HD + d);
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
-                        const float4 k4 = *reinterpret_cast<const float4*>(Ks + (4 * sub + u) * KP + d);
+                        const float4 k4 = *reinterpret_cast<const float4*>(Ks + (sub + 16 * u) * KP + d);
                         a[u] = __builtin_fmaf(q4.x, k4.x, a[u]);
                         a[u] = __builtin_fmaf(q4.y, k4.y, a[u]);
                         a[u] = __builtin_fmaf(q4.z, k4.z, a[u]);
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
             }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const int j = 4 * sub + u;
+                const int j = sub + 16 * u;
                 sc[u] = (row < nq && j < nk && j0 + j <= pos0 + i0 + row) ? a[u] * scale : -INFINITY;
             }
         }
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float e = sc[u] == -INFINITY ? 0.0f : expf(sc[u] - m);
-            Ps[row * ACH + 4 * sub + u] = e;
+            Ps[row * ACH + sub + 16 * u] = e;
             l += e;
         }
 #pragma unroll
@@ -211,56 +212,65 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
     if (!flag) return;
     float* Es = sm;  // [ATQ][nc_max] chunk weights e^(m_c - M)
     float* Os = sm + size_t(ATQ) * nc_max;  // [ATQ][HD] output rows
-    float inv = 0.0f;
-    if (row < nq) {
-        const int nci = (pos0 + i0 + row) / ACH + 1;
-        const size_t base = (size_t(i0 + row) * heads + head) * nc_max;
-        float M = -INFINITY;
-        for (int c0 = sub; c0 < nci; c0 += 64) {
-            float v[4];
+    // One round of loads: (m, l) of the row's chunks (lane-strided) and the first CB chunks of
+    // o for this thread's dims; then M, the weights e^(m_c - M) and L.
+    constexpr int CB = 16;
+    const int nci = row < nq ? (pos0 + i0 + row) / ACH + 1 : 0;
+    const size_t base = (size_t(i0 + row) * heads + head) * nc_max;
+    float ov[CB][DPT];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int c = c0 + 16 * u;
-                v[u] = c < nci ? ld_f32(rm, int((base + c) * 4)) : -INFINITY;
+    for (int k = 0; k < CB; k++)
+        if (k < nci) load_dpt<DPT>(ov[k], ro, int(((base + k) * HD + sub * DPT) * 4));
+    float inv = 0.0f;
+    {
+        // (m, l) of chunks sub + 16 u (u < 4) stay in registers; longer contexts reload the rest.
+        float mv[4], lv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int c = sub + 16 * u;
+            mv[u] = -INFINITY;
+            lv[u] = 0.0f;
+            if (c < nci) {
+                mv[u] = ld_f32(rm, int((base + c) * 4));
+                lv[u] = ld_f32(rl, int((base + c) * 4));
             }
-            M = fmaxf(M, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
         }
+        float M = fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3]));
+        for (int c = 64 + sub; c < nci; c += 16) M = fmaxf(M, ld_f32(rm, int((base + c) * 4)));
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
         float L = 0.0f;
-        for (int c0 = sub; c0 < nci; c0 += 64) {
-            float mv[4], lv[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int c = c0 + 16 * u;
-                mv[u] = lv[u] = 0.0f;
-                if (c < nci) {
-                    mv[u] = ld_f32(rm, int((base + c) * 4));
-                    lv[u] = ld_f32(rl, int((base + c) * 4));
-                }
+        for (int u = 0; u < 4; u++) {
+            const int c = sub + 16 * u;
+            if (c < nci) {
+                const float e = expf(mv[u] - M);
+                Es[row * nc_max + c] = e;
+                L = __builtin_fmaf(lv[u], e, L);
             }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int c = c0 + 16 * u;
-                if (c < nci) {
-                    const float e = expf(mv[u] - M);
-                    Es[row * nc_max + c] = e;
-                    L = __builtin_fmaf(lv[u], e, L);
-                }
-            }
+        }
+        for (int c = 64 + sub; c < nci; c += 16) {
+            const float e = expf(ld_f32(rm, int((base + c) * 4)) - M);
+            Es[row * nc_max + c] = e;
+            L = __builtin_fmaf(ld_f32(rl, int((base + c) * 4)), e, L);
         }
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) L += __shfl_xor(L, o, 64);
-        inv = 1.0f / L;
+        if (row < nq) inv = 1.0f / L;
     }
     __syncthreads();
     if (row < nq) {
-        const int nci = (pos0 + i0 + row) / ACH + 1;
-        const size_t base = (size_t(i0 + row) * heads + head) * nc_max;
         float o[DPT];
 #pragma unroll
         for (int u = 0; u < DPT; u++) o[u] = 0.0f;
-        for (int c0 = 0; c0 < nci; c0 += 8) {
+#pragma unroll
+        for (int k = 0; k < CB; k++)
+            if (k < nci) {
+                const float e = Es[row * nc_max + k];
+#pragma unroll
+                for (int u = 0; u < DPT; u++) o[u] = __builtin_fmaf(ov[k][u], e, o[u]);
+            }
+        for (int c0 = CB; c0 < nci; c0 += 8) {
             float v[8][DPT];
 #pragma unroll
             for (int k = 0; k < 8; k++)

@@ -539,6 +539,7 @@ void Model::check_request(const uint32_t* tok, size_t n) const {
 }
 
 // ---- profiling of the weight-streaming kernels ------------------------------------------
+// The next matrix launch records its own start and end (no marker packets in between).
 void Model::prof_begin() {
     if (!prof_) return;
     while (prof_ev_.size() < prof_used_ + 2) {
@@ -546,12 +547,11 @@ void Model::prof_begin() {
         HIPC(hipEventCreate(&e));
         prof_ev_.push_back(e);
     }
-    HIPC(hipEventRecord(prof_ev_[prof_used_], stream_));
+    mm_time_next_launch(prof_ev_[prof_used_], prof_ev_[prof_used_ + 1]);
 }
 
 void Model::prof_end(const TMat& W, int nt) {
     if (!prof_) return;
-    HIPC(hipEventRecord(prof_ev_[prof_used_ + 1], stream_));
     prof_used_ += 2;
     const Format f{W.bits, W.group};
     prof_acc_.launches++;
