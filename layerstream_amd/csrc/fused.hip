@@ -910,64 +910,63 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
     return blocks;
 }
 
-// One workgroup per token: every thread loads its share of the partials at once, then a shuffle
-// tree per wavefront and a scan over the wavefronts (the order does not matter: `beats` is a
-// total order).
-__global__ __launch_bounds__(256) void k_head_final(const float* __restrict__ pv, const int* __restrict__ pi, int arg_stride,
-                                                    int nblocks, const float* __restrict__ row0, uint32_t* __restrict__ amax) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int i = blockIdx.x, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const size_t base = size_t(i / FTOK) * arg_stride * FTOK + i % FTOK;
-    float v = NAN;
-    int ix = 0x7fffffff;
-    for (int b0 = threadIdx.x; b0 < nblocks; b0 += 8 * 256) {
-        float xv[8];
-        int xi[8];
+// One workgroup: wavefront w reduces tokens w, w + 16, ... (lane-strided partials, loads issued
+// eight at a time, then a shuffle tree; `beats` is a total order, so the grouping does not
+// matter). With a verify block, thread 0 then applies greedy acceptance (src/spec.rs:119-127):
+// m = first i < n - 1 with amax[i] != block[i + 1] (else n - 1), next = amax[m].
+__global__ __launch_bounds__(1024) void k_head_final(const float* __restrict__ pv, const int* __restrict__ pi, int arg_stride,
+                                                     int nblocks, const float* __restrict__ row0, int n,
+                                                     uint32_t* __restrict__ amax, const uint32_t* __restrict__ block,
+                                                     uint32_t* __restrict__ acc) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int i = w; i < n; i += 16) {
+        const size_t base = size_t(i / FTOK) * arg_stride * FTOK + i % FTOK;
+        float v = NAN;
+        int ix = 0x7fffffff;
+        for (int b0 = lane; b0 < nblocks; b0 += 8 * 64) {
+            float xv[8];
+            int xi[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int b = b0 + 256 * u;
-            xv[u] = NAN;
-            xi[u] = 0x7fffffff;
-            if (b < nblocks) {
-                xv[u] = pv[base + size_t(b) * FTOK];
-                xi[u] = pi[base + size_t(b) * FTOK];
+            for (int u = 0; u < 8; u++) {
+                const int b = b0 + 64 * u;
+                xv[u] = NAN;
+                xi[u] = 0x7fffffff;
+                if (b < nblocks) {
+                    xv[u] = pv[base + size_t(b) * FTOK];
+                    xi[u] = pi[base + size_t(b) * FTOK];
+                }
             }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (beats(xv[u], xi[u], v, ix)) {
+                    v = xv[u];
+                    ix = xi[u];
+                }
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (beats(xv[u], xi[u], v, ix)) {
-                v = xv[u];
-                ix = xi[u];
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o, 64);
+            const int oi = __shfl_xor(ix, o, 64);
+            if (beats(ov, oi, v, ix)) {
+                v = ov;
+                ix = oi;
             }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const int oi = __shfl_xor(ix, o, 64);
-        if (beats(ov, oi, v, ix)) {
-            v = ov;
-            ix = oi;
         }
+        if (lane == 0) amax[i] = isnan(row0[i]) ? 0u : uint32_t(ix);
     }
-    if (lane == 0) {
-        sv[w] = v;
-        si[w] = ix;
-    }
+    if (!block) return;
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 1; k < 4; k++)
-            if (beats(sv[k], si[k], v, ix)) {
-                v = sv[k];
-                ix = si[k];
-            }
-        amax[i] = isnan(row0[i]) ? 0u : uint32_t(ix);
+        int m = 0;
+        while (m < n - 1 && amax[m] == block[m + 1]) m++;
+        acc[0] = uint32_t(m);
+        acc[1] = amax[m];
     }
 }
 
 void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
-                       hipStream_t s) {
-    hipLaunchKernelGGL(k_head_final, dim3(n), dim3(256), 0, s, pv, pi, arg_stride, nblocks, row0, amax);
+                       const uint32_t* block, uint32_t* acc, hipStream_t s) {
+    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, pv, pi, arg_stride, nblocks, row0, n, amax, block, acc);
     FCHECK(hipGetLastError());
 }
 

@@ -136,8 +136,9 @@ void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream
 // partials at [tile][arg_off + b][16] for b below the returned count.
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // Final argmax over head-block partials (src/spec.rs:41-49 rule) for n tokens; row0 holds
-// logits[.][0].
+// logits[.][0]. With a verify block (device tokens, n of them) it also writes the greedy
+// acceptance acc[0] = m, acc[1] = next (src/spec.rs:119-127).
 void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
-                       hipStream_t s);
+                       const uint32_t* block, uint32_t* acc, hipStream_t s);
 
 }  // namespace ls

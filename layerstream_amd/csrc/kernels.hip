@@ -1,5 +1,5 @@
-// Small device kernels of the verify step for gfx950 (CDNA4, wave64): attention, greedy
-// acceptance and helpers. The weight-streaming kernels live in fused.hip.
+// Small device kernels of the verify step for gfx950 (CDNA4, wave64): attention and the
+// embedding helpers of streamed tables. The weight-streaming kernels live in fused.hip.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -371,19 +371,6 @@ __global__ void k_embed_raw(const uint8_t* __restrict__ raw, int bits, int group
 
 void embed_raw_rows(const uint8_t* raw, int bits, int group, int cols, int t, float* x, hipStream_t s) {
     hipLaunchKernelGGL(k_embed_raw, dim3(t), dim3(256), 0, s, raw, bits, group, cols, x);
-    HIPCHECK(hipGetLastError());
-}
-
-__global__ void k_accept(const uint32_t* __restrict__ amax, const uint32_t* __restrict__ block, int n, uint32_t* out) {
-    if (threadIdx.x != 0) return;
-    int m = 0;
-    while (m < n - 1 && amax[m] == block[m + 1]) m++;
-    out[0] = uint32_t(m);
-    out[1] = amax[m];
-}
-
-void accept_greedy(const uint32_t* amax, const uint32_t* block, int n, uint32_t* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_accept, dim3(1), dim3(64), 0, s, amax, block, n, out);
     HIPCHECK(hipGetLastError());
 }
 

@@ -1,4 +1,4 @@
-// Small device kernels of the verify step (gfx950): attention, acceptance, helpers.
+// Small device kernels of the verify step (gfx950): attention and embedding helpers.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,8 +22,5 @@ void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, 
 void bf16_to_f32_dev(const uint8_t* src, int n, float* dst, hipStream_t s);
 // x[t][cols] = dequantized raw embedding rows raw[t][row_bytes] (reference row layout).
 void embed_raw_rows(const uint8_t* raw, int bits, int group, int cols, int t, float* x, hipStream_t s);
-// Greedy acceptance (src/spec.rs:119-127): m = first i < n-1 with amax[i] != block[i+1] (else
-// n-1); next = amax[m]. Writes out[0] = m, out[1] = next.
-void accept_greedy(const uint32_t* amax, const uint32_t* block, int n, uint32_t* out, hipStream_t s);
 
 }  // namespace ls

@@ -504,12 +504,10 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     hpi_ = DevBuf(size_t(MAX_TILES) * head_blocks_ * FTOK * 4);
     row0_ = DevBuf(T * 4);
     amax_ = DevBuf(T * 4);
-    tok_ = DevBuf(max_ctx * 4);
+    stage_ = DevBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
     acc_ = DevBuf(16);
-    pos_dev_ = DevBuf((max_ctx / PREFILL_CHUNK + 2) * 4);
-    h_tok_ = PinnedBuf(max_ctx * 4);
+    h_stage_ = PinnedBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
     h_out_ = PinnedBuf(T * 4 + 16);
-    h_pos_ = PinnedBuf((max_ctx / PREFILL_CHUNK + 2) * 4);
     HIPC(hipStreamSynchronize(stream_));
 }
 
@@ -605,17 +603,22 @@ void Model::plan_kw_from_env() {
 
 // Copy a call's tokens (and the position of each 128-token chunk) to the device once. The
 // pinned staging buffers are only rewritten by the next call, after this call has drained.
+//
+// Staging layout, host (pinned) and device alike: [position of each 128-token chunk][tokens],
+// moved by one copy.
 const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
-    std::memcpy(h_tok_.p, tok, n * 4);
-    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
     const size_t chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
-    for (size_t ci = 0; ci < chunks; ci++) h_pos_.as<int>()[ci] = int(pos_ + ci * PREFILL_CHUNK);
-    HIPC(hipMemcpyAsync(pos_dev_.p, h_pos_.p, chunks * 4, hipMemcpyHostToDevice, stream_));
-    return tok_.as<uint32_t>();
+    int* hp = h_stage_.as<int>();
+    for (size_t ci = 0; ci < chunks; ci++) hp[ci] = int(pos_ + ci * PREFILL_CHUNK);
+    std::memcpy(hp + chunks, tok, n * 4);
+    HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, (chunks + n) * 4, hipMemcpyHostToDevice, stream_));
+    stage_pos_ = stage_.as<int>();
+    return reinterpret_cast<const uint32_t*>(stage_.as<int>() + chunks);
 }
 
 // forward_chunk (src/model.rs:161-220), all on the compute stream.
-void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits) {
+void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits,
+                          const uint32_t* accept_block) {
     const Config& c = cfg_;
     const int h = int(c.hidden), kv = int(c.kv_dim()), T = int(t);
     const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim);
@@ -624,7 +627,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     float* x = x_.as<float>();
     float* ss = ss_.as<float>();
     uint8_t* xf = xf_.as<uint8_t>();
-    const int* pos_dev = pos_dev_.as<int>() + chunk_index_;  // this chunk's first position
+    const int* pos_dev = stage_pos_ + chunk_index_;  // this chunk's first position
     const MMScratch scr{part_.as<float>(), cnt_.as<int>()};
     const bool res = prov_->resident();
     prov_->begin_forward(n_logits > 0);
@@ -750,7 +753,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             prof_end(hc.mat, nh);
             prov_->release_head_chunk(ci);
         }
-        head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(), s);
+        head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(),
+                          accept_block, acc_.as<uint32_t>(), s);
     }
     prov_->end_forward();
     pos_ += t;
@@ -794,10 +798,10 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
 }
 
 void Model::verify_body(const uint32_t* block, size_t n) {
-    HIPC(hipMemcpyAsync(tok_.p, h_tok_.p, n * 4, hipMemcpyHostToDevice, stream_));
-    HIPC(hipMemcpyAsync(pos_dev_.p, h_pos_.p, 4, hipMemcpyHostToDevice, stream_));
-    forward_chunk(block, tok_.as<uint32_t>(), n, n, false);
-    accept_greedy(amax_.as<uint32_t>(), tok_.as<uint32_t>(), int(n), acc_.as<uint32_t>(), stream_);
+    HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, (n + 1) * 4, hipMemcpyHostToDevice, stream_));
+    stage_pos_ = stage_.as<int>();
+    const uint32_t* dtok = reinterpret_cast<const uint32_t*>(stage_.as<int>() + 1);
+    forward_chunk(block, dtok, n, n, false, dtok);
     HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
 }
 
@@ -807,9 +811,10 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
     const size_t p = pos_;
     chunk_index_ = 0;
-    // Host staging; the previous call has drained, so the pinned buffers are free.
-    std::memcpy(h_tok_.p, block, n * 4);
-    h_pos_.as<int>()[0] = int(p);
+    // Host staging ([position][tokens], one chunk); the previous call has drained, so the
+    // pinned buffer is free.
+    h_stage_.as<int>()[0] = int(p);
+    std::memcpy(h_stage_.as<int>() + 1, block, n * 4);
     HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {
         auto it = graphs_.find(n);

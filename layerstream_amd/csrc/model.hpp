@@ -121,7 +121,10 @@ private:
     void check_request(const uint32_t* tok, size_t n) const;
     // Pushes t tokens through every layer; with n_logits > 0 also the head for the last rows,
     // logits stored when want_logits.
-    void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits);
+    // With accept_block (device tokens of a verify block) the argmax kernel also writes the
+    // greedy acceptance (m, next) to acc_.
+    void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits,
+                       const uint32_t* accept_block = nullptr);
     const uint32_t* stage_tokens(const uint32_t* tok, size_t n);
     // The device part of a verify step (token and position copies from the pinned staging
     // buffers, forward pass, acceptance, result copy): what a graph captures.
@@ -136,13 +139,14 @@ private:
     size_t max_ctx_, pos_ = 0, chunk_index_ = 0;
     hipStream_t stream_ = nullptr;
     std::unique_ptr<DeviceProvider> prov_;
-    DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_, pos_dev_;
+    DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_, stage_;
     // x_: residual rows; xf_/ss_: fragments and sum-of-squares partials of the next normalised
     // input; af_: attention output fragments; actf_: SiLU(g) * u fragments; part_/cnt_: split-K
     // scratch; hpv_/hpi_: head-block argmax partials; row0_: logits of row 0.
-    DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, tok_, acc_;
+    DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, acc_;
     int attn_splits_ = 1;
-    PinnedBuf h_tok_, h_out_, h_pos_;
+    PinnedBuf h_stage_, h_out_;
+    const int* stage_pos_ = nullptr;  // device positions of the staged chunks
     size_t vpad_ = 0, fb_h_ = 0, fb_q_ = 0, fb_in_ = 0;
     int head_blocks_ = 0, slots_h_ = 0;
     size_t head_off_ = 0;  // launch row of the first requested head row
