@@ -877,7 +877,13 @@ void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
     if ((a.heads + a.kv_heads) * a.hd % 16) throw std::runtime_error("q|k rows must fill whole strips");
     launch<EPI_QKV, 1>(a, p, sc, s);
 }
-void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) { launch<EPI_RESID, 1>(a, p, sc, s); }
+void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
+    switch (p.s) {
+        case 1: launch<EPI_RESID, 1>(a, p, sc, s); break;
+        case 2: launch<EPI_RESID, 2>(a, p, sc, s); break;
+        default: launch<EPI_RESID, 4>(a, p, sc, s); break;
+    }
+}
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     if (p.rg != 2) throw std::runtime_error("gate|up runs gate and up row blocks together");
     launch<EPI_SILU, GU_STRIPS>(a, p, sc, s);

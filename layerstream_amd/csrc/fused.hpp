@@ -127,7 +127,7 @@ struct MMScratch {
 // then v heads.
 void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // x[row] += W x; then fragments of x * onorm and sum-of-squares partials of the new rows (plan
-// strips 1).
+// strips 1, 2 or 4).
 void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan strips GU_STRIPS,
 // rg 2) + 1/rms + SiLU(g) * u -> act fragments.

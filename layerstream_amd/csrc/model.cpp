@@ -409,6 +409,9 @@ std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStr
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
 constexpr int MAX_TILES = int(PREFILL_CHUNK) / FTOK;
+// Strips per wavefront of the down projection: its K (the FFN width) is long and its rows few,
+// so two strips halve the input-fragment reads per weight byte.
+constexpr int DOWN_STRIPS = 2;
 
 Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx) {
@@ -484,7 +487,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
         const int n = int(T);
         const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(HEAD_ROWS), int(h), 256);
         const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1),        mm_plan(la.o, 1, kw_o_, n, 1),
-                                mm_plan(la.gu, 2, kw_gu_, n, GU_STRIPS), mm_plan(la.down, 1, kw_down_, n, 1),
+                                mm_plan(la.gu, 2, kw_gu_, n, GU_STRIPS), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS),
                                 mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};
         size_t pf = 0, nc = 0;
         for (const MMPlan& pl : plans) {
@@ -716,7 +719,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 a.oss_slots = slots_h_;
             }
             prof_begin();
-            mm_residual(a, mm_plan(L.down, 1, kw_down_, T, 1), scr, s);
+            mm_residual(a, mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS), scr, s);
             prof_end(L.down, T);
         }
         prov_->release_layer(l);
