@@ -40,4 +40,24 @@ __device__ __forceinline__ void write_slot(uint8_t* tile_frags, int ks, int ln, 
     o[128] = make_uint4(L[0], L[1], L[2], L[3]);
 }
 
+// The same slot written through the coherent (sc1) path, for fragments read by later workgroups
+// of the same launch. r covers the fragment buffer; tile_off is the tile's byte offset in it.
+__device__ __forceinline__ void write_slot_coherent(__amdgpu_buffer_rsrc_t r, size_t tile_off, int ks, int ln, const float* v) {
+    typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
+    uint32_t H[4], M[4], L[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        uint32_t h0, m0, l0, h1, m1, l1;
+        split3(v[j], h0, m0, l0);
+        split3(v[j + 1], h1, m1, l1);
+        H[j / 2] = h0 | (h1 << 16);
+        M[j / 2] = m0 | (m1 << 16);
+        L[j / 2] = l0 | (l1 << 16);
+    }
+    const int at = int(tile_off + (size_t(ks) * 3 * 64 + ln) * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4_{H[0], H[1], H[2], H[3]}, r, at, 0, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4_{M[0], M[1], M[2], M[3]}, r, at + 64 * 16, 0, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4_{L[0], L[1], L[2], L[3]}, r, at + 128 * 16, 0, 16);
+}
+
 }  // namespace ls

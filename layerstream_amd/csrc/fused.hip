@@ -373,16 +373,60 @@ constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
 constexpr int MAX_SPLIT = 16;
 constexpr int ROPE_HALF_MAX = 128;
 
+// Waits of the in-launch dataflow (see Flow). Thread 0 polls with atomic adds of zero: a plain
+// load, even at agent scope, can keep hitting this XCD's L2 copy of the line for microseconds,
+// while an atomic is served at the coherence point. The zero is hidden from the compiler, which
+// would otherwise turn the idempotent atomic back into a load. After a bounded number of sleeps
+// the wait records an error and goes on, so every wave ends.
+constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
+
+__device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
+    if (threadIdx.x == 0) {
+        int* cnt = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * j;
+        const int want = min(fl.producers, fl.per * (j + 1)) - fl.per * j;
+        int zero = 0;
+        asm volatile("" : "+v"(zero));
+        unsigned spins = 0;
+        while (__hip_atomic_fetch_add(cnt, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+            if (++spins > FLOW_SPIN_LIMIT) {
+                __hip_atomic_store(fl.ctl + FLOW_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        const int old = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == fl.consumers - 1) {
+            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+}
+
+// Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
+// moves.
+__device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (r / fl.per), 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
 // [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
 // 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half].
-template <int BITS, int EPI, bool G16, int S>
-__global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+// One matrix workgroup (row block bx / nsplit, K range bx % nsplit, token tile `tile`). With
+// IN_FLOW the input fragments come from earlier workgroups of the same launch: they are read
+// through the coherent path after waiting on fl. With OUT_FLOW (SiLU epilogue) the output
+// fragments are written through the coherent path and the workgroup then signals its counter.
+template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false>
+__device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const MMScratch& sc, const Flow& fl, int bx, int tile,
+                                        uint8_t* smem) {
     constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
-    extern __shared__ __align__(16) uint8_t smem[];
     const int nw = p.rg * p.kw, nthr = nw * 64;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int tile = blockIdx.y, rb = blockIdx.x / p.nsplit, sp = blockIdx.x % p.nsplit;
+    const int rb = bx / p.nsplit, sp = bx % p.nsplit;
     const int rows_wg = 16 * S * p.rg, row0 = rb * rows_wg;
     const int nt = min(FTOK, a.n - tile * FTOK);
     const TMat& W = a.W;
@@ -414,11 +458,13 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
         for (int c = 0; c < CPW; c++) {
             if (c < nch) {
                 load_chunk<S>(wb, sst, c0 + c, raw[c]);
+                if constexpr (!IN_FLOW) {
 #pragma unroll
-                for (int q = 0; q < Q; q++) {
-                    const int ks = (c0 + c) * Q + q;
+                    for (int q = 0; q < Q; q++) {
+                        const int ks = (c0 + c) * Q + q;
 #pragma unroll
-                    for (int t = 0; t < 3; t++) B[c * Q + q][t] = fb[(ks * 3 + t) * 64];
+                        for (int t = 0; t < 3; t++) B[c * Q + q][t] = fb[(ks * 3 + t) * 64];
+                    }
                 }
             }
         }
@@ -453,6 +499,26 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
         }
     }
     if (a.ss && wv == 0) inv_rms(a, tile, W.cols, inv);
+    if constexpr (IN_FLOW) {
+        // The weights are in flight; wait for the input, then read it coherently.
+        flow_wait(fl, sp);
+        const __amdgpu_buffer_rsrc_t rf =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.frags) + size_t(tile) * a.frag_stride, 0, int(a.frag_stride), BUF_DWORD3);
+#pragma unroll
+        for (int c = 0; c < CPW; c++) {
+            if (c < nch) {
+#pragma unroll
+                for (int q = 0; q < Q; q++) {
+                    const int ks = (c0 + c) * Q + q;
+#pragma unroll
+                    for (int t = 0; t < 3; t++) {
+                        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rf, ((ks * 3 + t) * 64 + lane) * 16, 0, CPOL_SC1);
+                        B[c * Q + q][t] = make_uint4(v[0], v[1], v[2], v[3]);
+                    }
+                }
+            }
+        }
+    }
 
     f32x4 total[S], acc[S];
 #pragma unroll
@@ -587,6 +653,7 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
     } else if constexpr (EPI == EPI_SILU) {
         // rows: [16 S gate rows | 16 S up rows] for act columns 16 S rb + [0, 16 S)
         uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
+        const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(a.ofrag_stride), BUF_DWORD3);
         for (int q = threadIdx.x; q < (2 * S) * FTOK; q += nthr) {
             const int cg = q / FTOK, tok = q % FTOK, col = 16 * S * rb + 8 * cg;
             float v[8];
@@ -602,8 +669,10 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
                     v[j] = __fmul_rn(g / (1.0f + expf(-g)), up);
                 }
             }
-            write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
+            if constexpr (OUT_FLOW) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
+            else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
+        if constexpr (OUT_FLOW) flow_signal(fl, rb);
     } else {
         // Output head: logits, optional store, per-token best (value, index) of this block.
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
@@ -648,6 +717,30 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
             a.arg_idx[at] = ix;
             if (rb == 0 && a.row0) a.row0[ibase + tok] = tl[tok];
         }
+    }
+}
+
+template <int BITS, int EPI, bool G16, int S>
+__global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, blockIdx.x, blockIdx.y, smem);
+}
+
+// gate|up and down in one launch (one token tile): workgroups [0, n_gu) run gate|up and count
+// themselves done once their SiLU fragments are stored; the down workgroups after them load
+// their weights, wait for the gate|up row blocks that produce their K range, then read the
+// fragments. Every gate|up workgroup has a lower index than every down workgroup, so it is
+// dispatched first and a waiting down workgroup never holds back one it waits for.
+template <int BITS, bool G16>
+__global__ __launch_bounds__(1024) void k_gu_down(MMArgs gu, MMPlan pgu, MMArgs dn, MMPlan pdn, MMScratch sc, Flow fl) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int ngu = pgu.nrb * pgu.nsplit;
+    if (int(blockIdx.x) < ngu) {
+        if (int(threadIdx.x) >= 64 * pgu.rg * pgu.kw) return;
+        mm_body<BITS, EPI_SILU, G16, GU_STRIPS, false, true>(gu, pgu, sc, fl, blockIdx.x, 0, smem);
+    } else {
+        if (int(threadIdx.x) >= 64 * pdn.rg * pdn.kw) return;
+        mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, false>(dn, pdn, sc, fl, blockIdx.x - ngu, 0, smem);
     }
 }
 
@@ -887,6 +980,40 @@ void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStrea
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     if (p.rg != 2) throw std::runtime_error("gate|up runs gate and up row blocks together");
     launch<EPI_SILU, GU_STRIPS>(a, p, sc, s);
+}
+
+void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, const MMPlan& pdn, const MMScratch& sc,
+                     int* ctl, hipStream_t s) {
+    if (pgu.rg != 2 || pgu.s != GU_STRIPS || pdn.s != DOWN_STRIPS) throw std::runtime_error("gate|up/down plans do not match");
+    if (pgu.tiles != 1 || pdn.tiles != 1) throw std::runtime_error("the fused gate|up/down launch takes one token tile");
+    if (pgu.nsplit != 1) throw std::runtime_error("the fused gate|up/down launch needs gate|up without a K split");
+    if (pdn.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
+    // A down K split covers 128 kw columns (4 k-steps of 32 per wavefront); a gate|up row block
+    // produces 16 GU_STRIPS of them.
+    const int split_cols = 128 * pdn.kw, act_cols = 16 * GU_STRIPS;
+    Flow fl;
+    fl.ctl = ctl;
+    fl.producers = pgu.nrb;
+    fl.per = split_cols / act_cols;
+    fl.consumers = pdn.nrb;
+    if (split_cols % act_cols || (fl.producers + fl.per - 1) / fl.per != pdn.nsplit || pdn.nsplit > FLOW_COUNTERS)
+        throw std::runtime_error("gate|up row blocks do not map onto the down K splits");
+    const int n = pgu.nrb * pgu.nsplit + pdn.nrb * pdn.nsplit;
+    const size_t lds = std::max(lds_bytes(pgu), lds_bytes(pdn));
+    const dim3 grid(n), block(64 * std::max(pgu.rg * pgu.kw, pdn.rg * pdn.kw));
+    const bool g16 = gu.W.bits != 16 && gu.W.group == 16;
+    switch (gu.W.bits) {
+        case 16: go(k_gu_down<16, false>, grid, block, lds, s, gu, pgu, dn, pdn, sc, fl); break;
+        case 8:
+            if (g16) go(k_gu_down<8, true>, grid, block, lds, s, gu, pgu, dn, pdn, sc, fl);
+            else go(k_gu_down<8, false>, grid, block, lds, s, gu, pgu, dn, pdn, sc, fl);
+            break;
+        default:
+            if (g16) go(k_gu_down<4, true>, grid, block, lds, s, gu, pgu, dn, pdn, sc, fl);
+            else go(k_gu_down<4, false>, grid, block, lds, s, gu, pgu, dn, pdn, sc, fl);
+            break;
+    }
+    FCHECK(hipGetLastError());
 }
 
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {

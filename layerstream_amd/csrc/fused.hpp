@@ -58,6 +58,9 @@ __host__ __device__ inline size_t frag_tile_bytes(int cols) { return size_t(tile
 __host__ __device__ inline int ss_slots(int cols) { return (cols + 15) / 16; }
 // gate|up rows are interleaved in blocks of 16 * GU_STRIPS (gate block, up block, ...).
 constexpr int GU_STRIPS = 2;
+// Strips per wavefront of the down projection: its K (the FFN width) is long and its rows few,
+// so two strips halve the input-fragment reads per weight byte.
+constexpr int DOWN_STRIPS = 2;
 
 // Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization) into
 // x [n][cols], plus fragments of x * w and sum-of-squares partials.
@@ -122,6 +125,21 @@ struct MMScratch {
     int* cnt = nullptr;
 };
 
+// In-launch dataflow between the two workgroup roles of a fused launch. Producer workgroup r
+// adds 1 to counter r / per once its output is stored; the consumers of counter j wait until it
+// reaches the number of producers that feed it, count themselves in the counter's second word,
+// and the last of `consumers` puts both words back to zero. Counters sit FLOW_CNT_STRIDE words
+// apart (their own cache lines). A wait that gives up sets the error word and goes on.
+struct Flow {
+    int* ctl = nullptr;  // control block, FLOW_WORDS ints, zero between launches
+    int producers = 0;
+    int per = 1;        // producers per counter
+    int consumers = 0;  // consumer workgroups per counter
+};
+// Control block words: error flag, greedy acceptance (m, next), then the counters.
+enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 16 };
+constexpr int FLOW_WORDS = FLOW_CNT0 + FLOW_CNT_STRIDE * FLOW_COUNTERS;
+
 // QKV projection + 1/rms + bias + RoPE + K/V append (plan strips 1). Rows: q heads and k heads
 // with each head's RoPE pairs adjacent (tile row 2j: dimension j, 2j + 1: dimension j + hd / 2),
 // then v heads.
@@ -132,6 +150,11 @@ void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStrea
 // gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan strips GU_STRIPS,
 // rg 2) + 1/rms + SiLU(g) * u -> act fragments.
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// gate|up then down (plan strips DOWN_STRIPS) in one launch for one token tile: each down K
+// split waits only for the gate|up row blocks that produce its columns. ctl is the control
+// block (FLOW_WORDS ints).
+void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, const MMPlan& pdn, const MMScratch& sc,
+                     int* ctl, hipStream_t s);
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
 // partials at [tile][arg_off + b][16] for b below the returned count.
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);

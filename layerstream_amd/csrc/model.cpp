@@ -409,9 +409,6 @@ std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStr
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
 constexpr int MAX_TILES = int(PREFILL_CHUNK) / FTOK;
-// Strips per wavefront of the down projection: its K (the FFN width) is long and its rows few,
-// so two strips halve the input-fragment reads per weight byte.
-constexpr int DOWN_STRIPS = 2;
 
 Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx) {
@@ -469,6 +466,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
         head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * HEAD_ROWS / 64));
     }
     plan_kw_from_env();
+    if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -508,9 +506,11 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     row0_ = DevBuf(T * 4);
     amax_ = DevBuf(T * 4);
     stage_ = DevBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
-    acc_ = DevBuf(16);
+    ctl_ = DevBuf(FLOW_WORDS * 4);
+    HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
     h_stage_ = PinnedBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
-    h_out_ = PinnedBuf(T * 4 + 16);
+    h_out_ = PinnedBuf(T * 4);
+    h_ctl_ = PinnedBuf(CTL_BACK * 4);
     HIPC(hipStreamSynchronize(stream_));
 }
 
@@ -551,11 +551,13 @@ void Model::prof_begin() {
     mm_time_next_launch(prof_ev_[prof_used_], prof_ev_[prof_used_ + 1]);
 }
 
-void Model::prof_end(const TMat& W, int nt) {
+void Model::prof_end(const TMat& W, int nt, bool launch) {
     if (!prof_) return;
-    prof_used_ += 2;
     const Format f{W.bits, W.group};
-    prof_acc_.launches++;
+    if (launch) {
+        prof_used_ += 2;
+        prof_acc_.launches++;
+    }
     prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * nt * (double(W.cols) + double(W.rows));
     prof_acc_.flops += 2.0 * nt * double(W.rows) * double(W.cols);
 }
@@ -688,39 +690,50 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             prof_end(L.o, T);
         }
         {
-            MMArgs a;
-            a.W = L.gu;
-            a.frags = xf;
-            a.frag_stride = fb_h_;
-            a.ss = ss;
-            a.ss_slots = slots_h_;
-            a.eps = c.eps;
-            a.n = T;
-            a.ofrags = actf_.as<uint8_t>();
-            a.ofrag_stride = fb_in_;
-            prof_begin();
-            mm_gate_up(a, mm_plan(L.gu, 2, kw_gu_, T, GU_STRIPS), scr, s);
-            prof_end(L.gu, T);
-        }
-        {
+            MMArgs g;
+            g.W = L.gu;
+            g.frags = xf;
+            g.frag_stride = fb_h_;
+            g.ss = ss;
+            g.ss_slots = slots_h_;
+            g.eps = c.eps;
+            g.n = T;
+            g.ofrags = actf_.as<uint8_t>();
+            g.ofrag_stride = fb_in_;
             const bool last = l + 1 == c.layers;
-            MMArgs a;
-            a.W = L.down;
-            a.frags = actf_.as<uint8_t>();
-            a.frag_stride = fb_in_;
-            a.n = T;
-            a.out = x;
-            a.ldo = h;
+            MMArgs d;
+            d.W = L.down;
+            d.frags = actf_.as<uint8_t>();
+            d.frag_stride = fb_in_;
+            d.n = T;
+            d.out = x;
+            d.ldo = h;
             if (last || res) {
-                a.ofrags = xf;
-                a.ofrag_stride = fb_h_;
-                a.onorm = last ? fnorm_.as<float>() : prov_->layer(l + 1).in_norm;
-                a.oss = ss;
-                a.oss_slots = slots_h_;
+                d.ofrags = xf;
+                d.ofrag_stride = fb_h_;
+                d.onorm = last ? fnorm_.as<float>() : prov_->layer(l + 1).in_norm;
+                d.oss = ss;
+                d.oss_slots = slots_h_;
             }
-            prof_begin();
-            mm_residual(a, mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS), scr, s);
-            prof_end(L.down, T);
+            const MMPlan pg = mm_plan(L.gu, 2, kw_gu_, T, GU_STRIPS), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS);
+            // Fused only when both roles fit on the device at one workgroup per CU (their
+            // wavefronts fill a CU's register file): a down workgroup that started after a
+            // gate|up one had finished would fetch its weights late. Either path gives the same
+            // bits (same plans).
+            if (fuse_on_ && pg.tiles == 1 && pg.nsplit == 1 && pg.nrb + pd.nrb * pd.nsplit <= device_cu_count()) {
+                // One launch: the down workgroups fetch their weights while gate|up runs.
+                prof_begin();
+                mm_gate_up_down(g, pg, d, pd, scr, ctl_.as<int>(), s);
+                prof_end(L.gu, T);
+                prof_end(L.down, T, false);
+            } else {
+                prof_begin();
+                mm_gate_up(g, pg, scr, s);
+                prof_end(L.gu, T);
+                prof_begin();
+                mm_residual(d, pd, scr, s);
+                prof_end(L.down, T);
+            }
         }
         prov_->release_layer(l);
     }
@@ -757,7 +770,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             prov_->release_head_chunk(ci);
         }
         head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(),
-                          accept_block, acc_.as<uint32_t>(), s);
+                          accept_block, reinterpret_cast<uint32_t*>(ctl_.as<int>() + FLOW_ACC), s);
     }
     prov_->end_forward();
     pos_ += t;
@@ -777,8 +790,10 @@ void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argm
     if (logits)
         HIPC(hipMemcpyAsync(logits, logits_.as<float>() + head_off_ * vpad_, cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
     if (argmax) HIPC(hipMemcpyAsync(h_out_.p, amax_.as<uint32_t>() + head_off_, 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
+    check_flow(h_ctl_.as<int>());
     if (argmax) *argmax = h_out_.as<uint32_t>()[0];
 }
 
@@ -795,8 +810,10 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
                               n_logits, hipMemcpyDeviceToHost, stream_));
     if (argmax)
         HIPC(hipMemcpyAsync(h_out_.p, amax_.as<uint32_t>() + head_off_, n_logits * 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
+    check_flow(h_ctl_.as<int>());
     if (argmax) std::memcpy(argmax, h_out_.p, n_logits * 4);
 }
 
@@ -805,7 +822,16 @@ void Model::verify_body(const uint32_t* block, size_t n) {
     stage_pos_ = stage_.as<int>();
     const uint32_t* dtok = reinterpret_cast<const uint32_t*>(stage_.as<int>() + 1);
     forward_chunk(block, dtok, n, n, false, dtok);
-    HIPC(hipMemcpyAsync(h_out_.p, acc_.p, 8, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, CTL_BACK * 4, hipMemcpyDeviceToHost, stream_));
+}
+
+// A fused launch whose wait gave up (it never does unless a producer workgroup could not run)
+// leaves garbage behind: report it and clear the control block for the next call.
+void Model::check_flow(const int* ctl) {
+    if (ctl[FLOW_ERR] == 0) return;
+    HIPC(hipMemsetAsync(ctl_.p, 0, FLOW_WORDS * 4, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    fail("a fused launch timed out waiting for its producers; the results of this call are invalid", LS_E_DEVICE);
 }
 
 void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t* next) {
@@ -849,7 +875,10 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     float ms = 0;
     HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
     last_step_ms_ = ms;
-    const uint32_t* o = h_out_.as<uint32_t>();
+    const int* ctl = h_ctl_.as<int>();
+    pos_ = p;
+    check_flow(ctl);
+    const uint32_t* o = reinterpret_cast<const uint32_t*>(ctl + FLOW_ACC);
     *m = o[0];
     *next = o[1];
     pos_ = p + o[0] + 1;  // truncate(p + m + 1), src/spec.rs:137-139
