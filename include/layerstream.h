@@ -148,6 +148,20 @@ int ls_model_forward_multi(ls_model* m, const uint32_t* tokens, size_t n, size_t
  * to the host. */
 int ls_model_verify_greedy(ls_model* m, const uint32_t* block, size_t n, uint32_t* accepted, uint32_t* next);
 
+/* Several independent sequences over one copy of the weights. The reference has one KV cache
+ * per Model (src/model.rs:16-26, 67-68); this model holds n_seq of them (each max_ctx tokens)
+ * and its own position per sequence. Every call above acts on the selected sequence (0 at
+ * creation). ls_model_create(...) is ls_model_create_batch(..., 1, ...). */
+int ls_model_create_batch(ls_source* src, int mode, int slots, size_t max_ctx, int device, int n_seq, ls_model** out);
+int ls_model_n_seq(const ls_model* m);
+int ls_model_select(ls_model* m, int seq);
+/* One verify pass over a block for every sequence (blocks concatenated in sequence order, lens[s]
+ * tokens for sequence s, each 1..33): the weights are read once for all of them. accepted[s] and
+ * next[s] are what ls_model_verify_greedy would return for that sequence alone, bit for bit, and
+ * each sequence is truncated to p_s + accepted[s] + 1 (src/spec.rs:116-139 per sequence). */
+int ls_model_verify_greedy_batch(ls_model* m, const uint32_t* blocks, const size_t* lens, int n_seq, uint32_t* accepted,
+                                 uint32_t* next);
+
 /* Provider report (src/provider.rs:29-37). */
 typedef struct {
     uint64_t resident_weight_bytes; /* device bytes held for weights */

@@ -120,6 +120,10 @@ SIGNATURES = {
     "ls_source_config": (C.c_int, [P, C.POINTER(Config)]),
     "ls_source_bytes_read": (C.c_uint64, [P]),
     "ls_model_create": (C.c_int, [P, C.c_int, C.c_int, SZ, C.c_int, C.POINTER(P)]),
+    "ls_model_create_batch": (C.c_int, [P, C.c_int, C.c_int, SZ, C.c_int, C.c_int, C.POINTER(P)]),
+    "ls_model_n_seq": (C.c_int, [P]),
+    "ls_model_select": (C.c_int, [P, C.c_int]),
+    "ls_model_verify_greedy_batch": (C.c_int, [P, U32, C.POINTER(SZ), C.c_int, U32, U32]),
     "ls_model_free": (None, [P]),
     "ls_model_pos": (SZ, [P]),
     "ls_model_max_ctx": (SZ, [P]),
@@ -324,12 +328,20 @@ class Source:
 
 
 class Model:
-    """Model (src/model.rs:16-140) on an MI355X. mode: MODE_RESIDENT or MODE_STREAM."""
+    """Model (src/model.rs:16-140) on an MI355X. mode: MODE_RESIDENT or MODE_STREAM.
 
-    def __init__(self, source: Source, mode: int = MODE_RESIDENT, slots: int = 2, max_ctx: int = 1024, device: int = 0):
+    With n_seq > 1 it holds that many independent sequences (K/V caches and positions) over one
+    copy of the weights: the single-sequence calls act on the selected one (select()), and
+    verify_greedy_batch() verifies a block of every sequence in one pass."""
+
+    def __init__(self, source: Source, mode: int = MODE_RESIDENT, slots: int = 2, max_ctx: int = 1024, device: int = 0,
+                 n_seq: int = 1):
         self.source = source
         h = C.c_void_p()
-        _check(lib().ls_model_create(source.h, mode, slots, max_ctx, device, C.byref(h)))
+        if n_seq == 1:
+            _check(lib().ls_model_create(source.h, mode, slots, max_ctx, device, C.byref(h)))
+        else:
+            _check(lib().ls_model_create_batch(source.h, mode, slots, max_ctx, device, n_seq, C.byref(h)))
         self.h = h
         self._cfg = source.config()
 
@@ -414,6 +426,27 @@ class Model:
     def use_graphs(self, enable: bool):
         """Replay verify steps from captured HIP graphs (default on; resident weights only)."""
         _check(lib().ls_model_use_graphs(self.h, int(enable)))
+
+    @property
+    def n_seq(self) -> int:
+        return lib().ls_model_n_seq(self.h)
+
+    def select(self, seq: int):
+        """Make sequence `seq` the one the single-sequence calls act on."""
+        _check(lib().ls_model_select(self.h, seq))
+
+    def verify_greedy_batch(self, blocks):
+        """One verify pass over blocks[s] for every sequence s: [(accepted m_s, next_s)], as
+        verify_greedy would return for each sequence alone; sequence s keeps p_s + m_s + 1."""
+        if len(blocks) != self.n_seq:
+            raise ValueError(f"{len(blocks)} blocks for {self.n_seq} sequences")
+        lens = np.array([len(b) for b in blocks], np.uint64)
+        flat = _toks(np.concatenate([np.asarray(b, np.uint32) for b in blocks]) if len(blocks) else [])
+        m = np.zeros(len(blocks), np.uint32)
+        nx = np.zeros(len(blocks), np.uint32)
+        _check(lib().ls_model_verify_greedy_batch(self.h, _u32(flat), lens.ctypes.data_as(C.POINTER(SZ)), len(blocks), _u32(m),
+                                                  _u32(nx)))
+        return [(int(a), int(b)) for a, b in zip(m, nx)]
 
 
 class ModelDrafter:

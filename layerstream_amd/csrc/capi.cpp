@@ -211,6 +211,39 @@ void ls_model_free(ls_model* m) {
     }
 }
 
+int ls_model_create_batch(ls_source* src, int mode, int slots, size_t max_ctx, int device, int n_seq, ls_model** out) {
+    return guard([&] {
+        need(src, "source");
+        need(out, "output");
+        auto m = std::make_unique<ls_model>();
+        m->m = std::make_unique<ls::Model>(*src->s, mode, slots, max_ctx, device, n_seq);
+        *out = m.release();
+    });
+}
+
+int ls_model_select(ls_model* m, int seq) {
+    return guard([&] {
+        need(m, "model");
+        m->m->select(seq);
+    });
+}
+
+int ls_model_n_seq(const ls_model* m) { return m ? m->m->n_seq() : 0; }
+
+int ls_model_verify_greedy_batch(ls_model* m, const uint32_t* blocks, const size_t* lens, int n_seq, uint32_t* accepted,
+                                 uint32_t* next) {
+    return guard([&] {
+        need(m, "model");
+        need(blocks, "blocks");
+        need(lens, "lens");
+        need(accepted, "accepted");
+        need(next, "next");
+        if (n_seq != m->m->n_seq())
+            ls::fail("the model holds " + std::to_string(m->m->n_seq()) + " sequences, not " + std::to_string(n_seq));
+        m->m->verify_greedy_batch(blocks, lens, accepted, next);
+    });
+}
+
 size_t ls_model_pos(const ls_model* m) { return m ? m->m->pos() : 0; }
 size_t ls_model_max_ctx(const ls_model* m) { return m ? m->m->max_ctx() : 0; }
 void ls_model_reset(ls_model* m) {

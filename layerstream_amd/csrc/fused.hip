@@ -415,7 +415,8 @@ __device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
 
 // Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
 // [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
-// 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half].
+// 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half, per-token position and
+// cache row 2 x 16].
 // One matrix workgroup (row block bx / nsplit, K range bx % nsplit, token tile `tile`). With
 // IN_FLOW the input fragments come from earlier workgroups of the same launch: they are read
 // through the coherent path after waiting on fl. With OUT_FLOW (SiLU epilogue) the output
@@ -445,6 +446,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     float* vec = xs + rows_wg * FTOK;
     float* rcos = vec + rows_wg;
     float* rsin = rcos + FTOK * ROPE_HALF_MAX;
+    int* tpos = reinterpret_cast<int*>(rsin + FTOK * ROPE_HALF_MAX);  // [position][cache row] per token
     const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
 
     // Every load of the wavefront's share is issued before any arithmetic.
@@ -470,7 +472,6 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         }
     }
     // Epilogue operands, staged in LDS while the weights are in flight.
-    int pos0 = 0;
     if constexpr (EPI == EPI_RESID) {
         for (int e0 = threadIdx.x; e0 < rows_wg * FTOK; e0 += 4 * nthr) {
             float xv[4];
@@ -490,10 +491,15 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         for (int r = threadIdx.x; r < rows_wg; r += nthr)
             vec[r] = row0 + r < W.rows ? a.bias[qkv_ref_row(row0 + r, a.hd, qk)] : 0.0f;
         const int half = a.hd / 2;
-        pos0 = *a.pos0;
+        const int pos0 = a.row_pos ? 0 : *a.pos0;
+        for (int tok = threadIdx.x; tok < nt; tok += nthr) {
+            const int i = ibase + tok, pos = a.row_pos ? a.row_pos[i] : pos0 + i;
+            tpos[tok] = pos;
+            tpos[FTOK + tok] = a.row_seq ? int(a.row_seq[i] * a.seq_stride) + pos : pos;
+        }
         for (int e = threadIdx.x; e < nt * half; e += nthr) {
-            const int tok = e / half, j = e % half;
-            const size_t at = size_t(pos0 + ibase + tok) * half + j;
+            const int tok = e / half, j = e % half, i = ibase + tok;
+            const size_t at = size_t(a.row_pos ? a.row_pos[i] : pos0 + i) * half + j;
             rcos[tok * half + j] = a.rope_cos[at];
             rsin[tok * half + j] = a.rope_sin[at];
         }
@@ -599,7 +605,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
             if (tok >= nt || row >= W.rows) continue;
-            const int i = ibase + tok, pos = pos0 + i;
+            const int i = ibase + tok, crow = tpos[FTOK + tok];  // cache row
             const float iv = a.ss ? inv[tok] : 1.0f;
             float v = __fadd_rn(a.ss ? __fmul_rn(tl[e], iv) : tl[e], vec[rl]);
             int ref = row;
@@ -616,8 +622,8 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 }
             }
             if (ref < h) a.out[size_t(i) * a.ldo + ref] = v;
-            else if (ref < h + kvd) a.kcache[size_t(pos) * kvd + (ref - h)] = v;
-            else a.vcache[size_t(pos) * kvd + (ref - h - kvd)] = v;
+            else if (ref < h + kvd) a.kcache[size_t(crow) * kvd + (ref - h)] = v;
+            else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
         }
     } else if constexpr (EPI == EPI_RESID) {
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
@@ -923,7 +929,7 @@ size_t mm_counters(const MMPlan& p) { return p.nsplit > 1 ? size_t(p.tiles) * p.
 static size_t lds_bytes(const MMPlan& p) {
     const size_t red = p.kw > 1 ? size_t(p.rg) * p.kw * p.s * 64 * 16 : 0;
     const size_t rows = size_t(16 * p.s * p.rg);
-    return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX) * 4;
+    return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX + 2 * FTOK) * 4;
 }
 
 static thread_local hipEvent_t t_start = nullptr, t_stop = nullptr;
@@ -1043,16 +1049,17 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
     return blocks;
 }
 
-// One workgroup: wavefront w reduces tokens w, w + 16, ... (lane-strided partials, loads issued
-// eight at a time, then a shuffle tree; `beats` is a total order, so the grouping does not
-// matter). With a verify block, thread 0 then applies greedy acceptance (src/spec.rs:119-127):
-// m = first i < n - 1 with amax[i] != block[i + 1] (else n - 1), next = amax[m].
+// Wavefront w of workgroup b reduces tokens 16 b + w, then 16 more workgroups on (lane-strided
+// partials, loads issued eight at a time, then a shuffle tree; `beats` is a total order, so the
+// grouping does not matter). With a verify block (one workgroup), thread 0 then applies greedy
+// acceptance (src/spec.rs:119-127): m = first i < n - 1 with amax[i] != block[i + 1] (else
+// n - 1), next = amax[m].
 __global__ __launch_bounds__(1024) void k_head_final(const float* __restrict__ pv, const int* __restrict__ pi, int arg_stride,
                                                      int nblocks, const float* __restrict__ row0, int n,
                                                      uint32_t* __restrict__ amax, const uint32_t* __restrict__ block,
                                                      uint32_t* __restrict__ acc) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    for (int i = w; i < n; i += 16) {
+    for (int i = blockIdx.x * 16 + w; i < n; i += 16 * gridDim.x) {
         const size_t base = size_t(i / FTOK) * arg_stride * FTOK + i % FTOK;
         float v = NAN;
         int ix = 0x7fffffff;
@@ -1099,7 +1106,28 @@ __global__ __launch_bounds__(1024) void k_head_final(const float* __restrict__ p
 
 void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
                        const uint32_t* block, uint32_t* acc, hipStream_t s) {
-    hipLaunchKernelGGL(k_head_final, dim3(1), dim3(1024), 0, s, pv, pi, arg_stride, nblocks, row0, n, amax, block, acc);
+    // One workgroup when it also decides the acceptance (which needs every row), else one per
+    // 16 rows.
+    const int nwg = block ? 1 : (n + 15) / 16;
+    hipLaunchKernelGGL(k_head_final, dim3(nwg), dim3(1024), 0, s, pv, pi, arg_stride, nblocks, row0, n, amax, block, acc);
+    FCHECK(hipGetLastError());
+}
+
+__global__ void k_accept_batch(const uint32_t* __restrict__ amax, const uint32_t* __restrict__ tok, const int* __restrict__ first,
+                               const int* __restrict__ len, int n_seq, const int* __restrict__ ctl, uint32_t* __restrict__ out) {
+    for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < n_seq; q += gridDim.x * blockDim.x) {
+        const int f = first[q], n = len[q];
+        int m = 0;
+        while (m < n - 1 && amax[f + m] == tok[f + m + 1]) m++;
+        out[1 + 2 * q] = uint32_t(m);
+        out[2 + 2 * q] = amax[f + m];
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = uint32_t(ctl[FLOW_ERR]);
+}
+
+void accept_greedy_batch(const uint32_t* amax, const uint32_t* tok, const int* first, const int* len, int n_seq, const int* ctl,
+                         uint32_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_accept_batch, dim3(1), dim3(256), 0, s, amax, tok, first, len, n_seq, ctl, out);
     FCHECK(hipGetLastError());
 }
 

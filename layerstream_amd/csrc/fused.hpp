@@ -88,6 +88,12 @@ struct MMArgs {
     const float* rope_cos = nullptr;
     const float* rope_sin = nullptr;
     const int* pos0 = nullptr;  // device scalar: position of token 0 of the launch
+    // Rows of several sequences (device, per launch row; null for one sequence): row i sits at
+    // position row_pos[i] of sequence row_seq[i], whose K/V rows start seq_stride rows into the
+    // caches.
+    const int* row_pos = nullptr;
+    const int* row_seq = nullptr;
+    size_t seq_stride = 0;
     int heads = 0, kv_heads = 0, hd = 0;
     // output fragments and sum-of-squares partials (residual: of x * onorm; SiLU: of act)
     uint8_t* ofrags = nullptr;
@@ -163,5 +169,11 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
 // acceptance acc[0] = m, acc[1] = next (src/spec.rs:119-127).
 void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nblocks, const float* row0, int n, uint32_t* amax,
                        const uint32_t* block, uint32_t* acc, hipStream_t s);
+
+// Greedy acceptance of several verify blocks from the argmax of every launch row: block s
+// holds rows [first[s], first[s] + len[s]) with tokens tok (src/spec.rs:119-127 per block).
+// out = [ctl[FLOW_ERR], m_0, next_0, m_1, next_1, ...].
+void accept_greedy_batch(const uint32_t* amax, const uint32_t* tok, const int* first, const int* len, int n_seq, const int* ctl,
+                         uint32_t* out, hipStream_t s);
 
 }  // namespace ls

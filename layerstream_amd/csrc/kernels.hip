@@ -25,10 +25,12 @@ namespace ls {
 // reference computes scores (q . k_j) * scale, a softmax (max, exp(x - max), sum, * 1/sum) and
 // sum_j p_j v_j over every cached position.
 //
-// One launch: grid (ASPLIT, heads, token tiles). Workgroup s takes chunks s, s + ASPLIT, ...
-// of its (head, tile) in order and keeps a running (max, sum, output) per token (online
-// softmax); the last of the ASPLIT workgroups to finish (an agent-scope counter) merges their
-// states in workgroup order and writes the output rows as fragments. Scores and the weighted
+// One launch: grid (ASPLIT, heads, row segments). A segment is a run of at most 16 consecutive
+// rows of one sequence inside one 16-row tile: every token tile of a single sequence, or the
+// pieces of a batch of sequences cut at tile boundaries. Workgroup s takes chunks s,
+// s + ASPLIT, ... of its (head, segment) in order and keeps a running (max, sum, output) per
+// token (online softmax); the last of the ASPLIT workgroups to finish (an agent-scope counter)
+// merges their states in workgroup order and writes the output rows as fragments. Scores and the weighted
 // sum run on v_mfma_f32_16x16x4f32 (f32 products and sums): scores as [keys][tokens], one
 // 16-key block per wavefront; the output as [dims][tokens], one 16-dim block per wavefront.
 // Which chunks a workgroup takes depends only on key positions and ASPLIT, so a token's result
@@ -71,9 +73,11 @@ struct AttnLds {
     static constexpr int K = 0, V = K + ACH * KP, Q = V + ACH * VP, P = Q + ATQ * QP, R = P + ACH * ATQ, END = R + 2 * 4 * ATQ;
 };
 
+// Segment z: without a table, token tile z of one sequence whose row 0 sits at *pos0; with
+// one, segs[z] = (first row, rows, sequence, -) and each row's position is rows.pos[row].
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int ldq, int t, int heads, int kv_heads,
-                                              const int* __restrict__ pos0p, float scale, const float* __restrict__ kc,
+                                              const int* __restrict__ pos0p, AttnRows rows, float scale, const float* __restrict__ kc,
                                               const float* __restrict__ vc, float* pm, float* pl, float* po, int* cnt,
                                               uint8_t* __restrict__ frags, size_t frag_stride) {
     using LY = AttnLds<HD>;
@@ -89,12 +93,24 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
     float* Ps = sm + LY::P;   // [key][token]
     float* Rm = sm + LY::R;   // [wave][token] chunk maxima
     float* Rl = Rm + 4 * ATQ; // [wave][token] chunk sums
-    const int s = blockIdx.x, head = blockIdx.y, tile = blockIdx.z, i0 = tile * ATQ;
+    const int s = blockIdx.x, head = blockIdx.y, seg = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, tok = lane & 15, g = lane >> 4;
     const int kv = kv_heads * HD, grp = head / (heads / kv_heads);
-    const int nq = min(ATQ, t - i0);
-    const int pos0 = *pos0p;
-    const int last_key = pos0 + i0 + nq - 1;
+    int i0, nq, pos_first;  // first launch row, rows, position of the first row
+    if (rows.segs) {
+        const int4 sg = rows.segs[seg];
+        i0 = sg.x;
+        nq = sg.y;
+        pos_first = rows.pos[i0];
+        kc += size_t(sg.z) * rows.seq_stride;
+        vc += size_t(sg.z) * rows.seq_stride;
+    } else {
+        i0 = seg * ATQ;
+        nq = min(ATQ, t - i0);
+        pos_first = *pos0p + i0;
+    }
+    const int tile = i0 / ATQ, tok0 = i0 % ATQ;  // fragment tile and token of the first row
+    const int last_key = pos_first + nq - 1;
     const int nc = last_key / ACH + 1;
     const size_t rows_total = size_t(t) * heads;
     const __amdgpu_buffer_rsrc_t rm = coherent_rsrc(pm, rows_total * ASPLIT * 4);
@@ -158,7 +174,7 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int j = 16 * w + 4 * g + i;
-            sv[i] = (tok < nq && j < nk && j0 + j <= pos0 + i0 + tok) ? sc[i] * scale : -INFINITY;
+            sv[i] = (tok < nq && j < nk && j0 + j <= pos_first + tok) ? sc[i] * scale : -INFINITY;
             mx = fmaxf(mx, sv[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -214,11 +230,11 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
         }
     }
 
-    // The last workgroup of (head, tile) merges the ASPLIT states in order.
+    // The last workgroup of (head, segment) merges the ASPLIT states in order.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        int* cn = cnt + size_t(tile) * heads + head;
+        int* cn = cnt + size_t(seg) * heads + head;
         const int old = __hip_atomic_fetch_add(cn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int last = old == ASPLIT - 1;
         if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -271,38 +287,39 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
     uint8_t* tf = frags + size_t(tile) * frag_stride;
     for (int p = tid; p < nq * (HD / 8); p += 256) {
         const int i = p / (HD / 8), sl = p % (HD / 8), col = head * HD + 8 * sl;
-        write_slot(tf, col / 32, i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
+        write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
     }
 }
 
 size_t attention_scratch_floats(int t, int heads, int hd, int) { return size_t(t) * heads * ASPLIT * (hd + 2); }
 
 template <int HD>
-static void launch_attn(const float* q, int ldq, int t, int heads, int kv_heads, const int* pos0, const float* kc,
-                        const float* vc, float* scratch, int* cnt, uint8_t* frags, hipStream_t s) {
+static void launch_attn(const float* q, int ldq, int t, int heads, int kv_heads, const int* pos0, const AttnRows& rows,
+                        const float* kc, const float* vc, float* scratch, int* cnt, uint8_t* frags, hipStream_t s) {
     float* pm = scratch;
     float* pl = pm + size_t(t) * heads * ASPLIT;
     float* po = pl + size_t(t) * heads * ASPLIT;
     using LY = AttnLds<HD>;
     const size_t lds = sizeof(float) * size_t(LY::END);
     const float scale = 1.0f / sqrtf(float(HD));
-    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, (t + ATQ - 1) / ATQ), dim3(256), lds, s, q, ldq, t, heads, kv_heads, pos0,
+    const int nseg = rows.segs ? rows.n_segs : (t + ATQ - 1) / ATQ;
+    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(256), lds, s, q, ldq, t, heads, kv_heads, pos0, rows,
                        scale, kc, vc, pm, pl, po, cnt, frags, frag_tile_bytes(heads * HD));
     HIPCHECK(hipGetLastError());
 }
 
-void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, const int* pos0, int, const float* k_cache,
-               const float* v_cache, float* scratch, int* cnt, int, uint8_t* frags, hipStream_t s) {
+void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, const int* pos0, const AttnRows& rows,
+               const float* k_cache, const float* v_cache, float* scratch, int* cnt, uint8_t* frags, hipStream_t s) {
+    if (rows.segs && rows.n_segs <= 0) throw std::runtime_error("attention: empty segment table");
     switch (hd) {
-        case 16: launch_attn<16>(q, ldq, t, heads, kv_heads, pos0, k_cache, v_cache, scratch, cnt, frags, s); break;
-        case 32: launch_attn<32>(q, ldq, t, heads, kv_heads, pos0, k_cache, v_cache, scratch, cnt, frags, s); break;
-        case 64: launch_attn<64>(q, ldq, t, heads, kv_heads, pos0, k_cache, v_cache, scratch, cnt, frags, s); break;
-        case 128: launch_attn<128>(q, ldq, t, heads, kv_heads, pos0, k_cache, v_cache, scratch, cnt, frags, s); break;
+        case 16: launch_attn<16>(q, ldq, t, heads, kv_heads, pos0, rows, k_cache, v_cache, scratch, cnt, frags, s); break;
+        case 32: launch_attn<32>(q, ldq, t, heads, kv_heads, pos0, rows, k_cache, v_cache, scratch, cnt, frags, s); break;
+        case 64: launch_attn<64>(q, ldq, t, heads, kv_heads, pos0, rows, k_cache, v_cache, scratch, cnt, frags, s); break;
+        case 128: launch_attn<128>(q, ldq, t, heads, kv_heads, pos0, rows, k_cache, v_cache, scratch, cnt, frags, s); break;
         default: throw std::runtime_error("head_dim must be 16, 32, 64 or 128");
     }
 }
 
-int attention_splits(int) { return ASPLIT; }
 
 __global__ void k_bf16_to_f32(const uint8_t* __restrict__ src, int n, float* __restrict__ dst) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;

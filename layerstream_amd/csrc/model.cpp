@@ -226,8 +226,8 @@ class StreamProvider : public DeviceProvider {
     };
 
 public:
-    StreamProvider(const Source& src, int slots, hipStream_t compute)
-        : src_(src), c_(src.cfg()), L_(src.layout()), a_(layer_arena(c_)), compute_(compute) {
+    StreamProvider(const Source& src, int slots, size_t max_rows, hipStream_t compute)
+        : src_(src), c_(src.cfg()), L_(src.layout()), a_(layer_arena(c_)), compute_(compute), max_rows_(max_rows) {
         if (slots < 1) slots = 1;
         HIPC(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking));
         const size_t rb = c_.row_bytes();
@@ -248,8 +248,8 @@ public:
             HIPC(hipEventCreateWithFlags(&s.freed, hipEventDisableTiming));
         }
         HIPC(hipStreamSynchronize(copy_));
-        embed_stage_ = PinnedBuf(128 * rb);
-        embed_raw_ = DevBuf(128 * rb);
+        embed_stage_ = PinnedBuf(max_rows_ * rb);
+        embed_raw_ = DevBuf(max_rows_ * rb);
         HIPC(hipEventCreateWithFlags(&embed_copied_, hipEventDisableTiming));
     }
     ~StreamProvider() override {
@@ -302,6 +302,7 @@ public:
     void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x, const float* w, uint8_t* frags, float* ss) override {
         // Rows come from the source on every pass, as src/provider.rs:284-286.
         const size_t rb = c_.row_bytes();
+        if (size_t(t) > max_rows_) fail("more embedding rows than the staging buffer holds", LS_E_STATE);
         HIPC(hipEventSynchronize(embed_copied_));
         for (int i = 0; i < t; i++) src_.read_embed_rows(host_tokens[i], 1, embed_stage_.as<uint8_t>() + size_t(i) * rb);
         HIPC(hipMemcpyAsync(embed_raw_.p, embed_stage_.p, size_t(t) * rb, hipMemcpyHostToDevice, compute_));
@@ -391,6 +392,7 @@ private:
     size_t next_issue_ = 0, next_take_ = 0, buf_size_ = 0;
     bool holding_ = false;
     DevLayer cur_layer_;
+    size_t max_rows_;
     PinnedBuf embed_stage_;
     DevBuf embed_raw_;
     hipEvent_t embed_copied_ = nullptr;
@@ -400,19 +402,25 @@ private:
 std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t s) {
     return std::make_unique<ResidentProvider>(src, s);
 }
-std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStream_t s) {
-    return std::make_unique<StreamProvider>(src, slots, s);
+std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, size_t max_rows, hipStream_t s) {
+    return std::make_unique<StreamProvider>(src, slots, max_rows, s);
 }
 
 // ---------------------------------------------------------------------------------------
 // Model
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
-constexpr int MAX_TILES = int(PREFILL_CHUNK) / FTOK;
+constexpr size_t MAX_BLOCK = 33;       // a verify block: 1 + MAX_DRAFT (src/spec.rs:52) tokens
+constexpr int MAX_SEQ = 1024;
 
-Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
-    : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx) {
+Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device, int n_seq)
+    : cfg_(src.cfg()), device_(device), max_ctx_(max_ctx), n_seq_(n_seq) {
     if (max_ctx == 0) fail("max_ctx must be positive");
+    if (n_seq < 1 || n_seq > MAX_SEQ) fail("a model holds 1 to " + std::to_string(MAX_SEQ) + " sequences");
+    if (size_t(n_seq) * max_ctx > size_t(INT32_MAX / 2)) fail("sequences x max_ctx is too large");
+    seq_pos_.assign(size_t(n_seq), 0);
+    // Launch rows: a prefill chunk, or one block of up to MAX_BLOCK tokens per sequence.
+    rows_cap_ = (std::max(PREFILL_CHUNK, size_t(n_seq) * MAX_BLOCK) + FTOK - 1) / FTOK * FTOK;
     const Config& c = cfg_;
     if (c.inter % 64 != 0) fail("the intermediate size must be a multiple of 64");
     if (c.head_dim != 16 && c.head_dim != 32 && c.head_dim != 64 && c.head_dim != 128)
@@ -423,12 +431,14 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     HIPC(hipEventCreate(&ev0_));
     HIPC(hipEventCreate(&ev1_));
     if (mode == LS_MODE_RESIDENT) prov_ = make_resident(src, stream_);
-    else if (mode == LS_MODE_STREAM) prov_ = make_stream(src, slots, stream_);
+    else if (mode == LS_MODE_STREAM) prov_ = make_stream(src, slots, rows_cap_, stream_);
     else fail("unknown mode " + std::to_string(mode) + " (use resident or stream)");
 
-    const size_t h = c.hidden, kv = c.kv_dim(), in = c.inter, T = PREFILL_CHUNK;
-    kcache_ = DevBuf(c.layers * max_ctx * kv * 4);
-    vcache_ = DevBuf(c.layers * max_ctx * kv * 4);
+    const size_t h = c.hidden, kv = c.kv_dim(), in = c.inter, T = rows_cap_;
+    const size_t tiles = T / FTOK, max_segs = tiles + size_t(n_seq);
+    // K/V caches [layer][sequence][position][kv_dim].
+    kcache_ = DevBuf(c.layers * n_seq * max_ctx * kv * 4);
+    vcache_ = DevBuf(c.layers * n_seq * max_ctx * kv * 4);
     HIPC(hipMemsetAsync(kcache_.p, 0, kcache_.n, stream_));
     HIPC(hipMemsetAsync(vcache_.p, 0, vcache_.n, stream_));
 
@@ -470,16 +480,16 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
-    xf_ = DevBuf(fb_h_ * MAX_TILES);
-    ss_ = DevBuf(size_t(MAX_TILES) * slots_h_ * FTOK * 4);
-    af_ = DevBuf(fb_q_ * MAX_TILES);
-    actf_ = DevBuf(fb_in_ * MAX_TILES);
+    xf_ = DevBuf(fb_h_ * tiles);
+    ss_ = DevBuf(tiles * slots_h_ * FTOK * 4);
+    af_ = DevBuf(fb_q_ * tiles);
+    actf_ = DevBuf(fb_in_ * tiles);
     HIPC(hipMemsetAsync(xf_.p, 0, xf_.n, stream_));
     HIPC(hipMemsetAsync(ss_.p, 0, ss_.n, stream_));
     HIPC(hipMemsetAsync(af_.p, 0, af_.n, stream_));
     HIPC(hipMemsetAsync(actf_.p, 0, actf_.n, stream_));
     {
-        // Split-K scratch for the largest launch of each matrix (PREFILL_CHUNK tokens).
+        // Split-K scratch for the largest launch of each matrix (T rows).
         const LayerArena la = layer_arena(c);
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const int n = int(T);
@@ -497,31 +507,42 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device)
         HIPC(hipMemsetAsync(cnt_.p, 0, cnt_.n, stream_));
     }
     attn_scratch_ = DevBuf(attention_scratch_floats(int(T), int(c.heads), int(c.head_dim), int(max_ctx)) * 4);
-    attn_splits_ = attention_splits(int(max_ctx));
-    attn_cnt_ = DevBuf(size_t(MAX_TILES) * c.heads * 4);
+    attn_cnt_ = DevBuf(max_segs * c.heads * 4);
     HIPC(hipMemsetAsync(attn_cnt_.p, 0, attn_cnt_.n, stream_));
-    logits_ = DevBuf(T * vpad_ * 4);
-    hpv_ = DevBuf(size_t(MAX_TILES) * head_blocks_ * FTOK * 4);
-    hpi_ = DevBuf(size_t(MAX_TILES) * head_blocks_ * FTOK * 4);
+    logits_ = DevBuf(PREFILL_CHUNK * vpad_ * 4);  // logits are returned for at most one chunk
+    hpv_ = DevBuf(tiles * head_blocks_ * FTOK * 4);
+    hpi_ = DevBuf(tiles * head_blocks_ * FTOK * 4);
     row0_ = DevBuf(T * 4);
     amax_ = DevBuf(T * 4);
-    stage_ = DevBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
+    // Staging (ints): a call's chunk positions and tokens, or a batch's segments, rows and blocks.
+    const size_t stage_words = std::max(max_ctx / PREFILL_CHUNK + 2 + max_ctx, 4 * max_segs + 3 * T + 2 * size_t(n_seq));
+    stage_ = DevBuf(stage_words * 4);
     ctl_ = DevBuf(FLOW_WORDS * 4);
     HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
-    h_stage_ = PinnedBuf((max_ctx / PREFILL_CHUNK + 2 + max_ctx) * 4);
-    h_out_ = PinnedBuf(T * 4);
+    bacc_ = DevBuf((1 + 2 * size_t(n_seq)) * 4);
+    h_stage_ = PinnedBuf(stage_words * 4);
+    h_out_ = PinnedBuf(PREFILL_CHUNK * 4);
     h_ctl_ = PinnedBuf(CTL_BACK * 4);
+    h_bacc_ = PinnedBuf((1 + 2 * size_t(n_seq)) * 4);
     HIPC(hipStreamSynchronize(stream_));
 }
 
 Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : batch_graphs_) (void)hipGraphExecDestroy(kv.second);
     for (hipEvent_t e : prof_ev_) (void)hipEventDestroy(e);
     prov_.reset();
     if (ev0_) (void)hipEventDestroy(ev0_);
     if (ev1_) (void)hipEventDestroy(ev1_);
     if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Model::select(int seq) {
+    if (seq < 0 || seq >= n_seq_) fail("sequence " + std::to_string(seq) + " is not in [0, " + std::to_string(n_seq_) + ")");
+    seq_pos_[size_t(cur_)] = pos_;
+    cur_ = seq;
+    pos_ = seq_pos_[size_t(seq)];
 }
 
 void Model::truncate(size_t pos) {
@@ -623,7 +644,7 @@ const uint32_t* Model::stage_tokens(const uint32_t* tok, size_t n) {
 
 // forward_chunk (src/model.rs:161-220), all on the compute stream.
 void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits,
-                          const uint32_t* accept_block) {
+                          const uint32_t* accept_block, const BatchView* bv) {
     const Config& c = cfg_;
     const int h = int(c.hidden), kv = int(c.kv_dim()), T = int(t);
     const int heads = int(c.heads), kvh = int(c.kv_heads), hd = int(c.head_dim);
@@ -643,8 +664,10 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr);
     for (size_t l = 0; l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
-        float* kc = kcache_.as<float>() + l * max_ctx_ * kv;
-        float* vc = vcache_.as<float>() + l * max_ctx_ * kv;
+        // This layer's caches: every sequence's for a batch, else the selected one's.
+        const size_t cache_off = (l * size_t(n_seq_) + (bv ? 0 : size_t(cur_))) * max_ctx_ * kv;
+        float* kc = kcache_.as<float>() + cache_off;
+        float* vc = vcache_.as<float>() + cache_off;
         if (!res) x_frags(x, T, h, L.in_norm, xf, ss, s);
         {
             MMArgs a;
@@ -663,6 +686,11 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.rope_cos = rope_cos_.as<float>();
             a.rope_sin = rope_sin_.as<float>();
             a.pos0 = pos_dev;
+            if (bv) {
+                a.row_pos = bv->pos;
+                a.row_seq = bv->seq;
+                a.seq_stride = max_ctx_;
+            }
             a.heads = heads;
             a.kv_heads = kvh;
             a.hd = hd;
@@ -670,8 +698,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             mm_qkv(a, mm_plan(L.qkv, 1, kw_qkv_, T, 1), scr, s);
             prof_end(L.qkv, T);
         }
-        attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, int(max_ctx_), kc, vc, attn_scratch_.as<float>(), attn_cnt_.as<int>(),
-                  attn_splits_, af_.as<uint8_t>(), s);
+        attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, bv ? bv->attn : AttnRows{}, kc, vc, attn_scratch_.as<float>(),
+                  attn_cnt_.as<int>(), af_.as<uint8_t>(), s);
         {
             MMArgs a;
             a.W = L.o;
@@ -773,7 +801,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                           accept_block, reinterpret_cast<uint32_t*>(ctl_.as<int>() + FLOW_ACC), s);
     }
     prov_->end_forward();
-    pos_ += t;
+    if (!bv) pos_ += t;
 }
 
 void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax) {
@@ -839,6 +867,7 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     check_request(block, n);
     if (n > PREFILL_CHUNK) fail("a verify block takes at most 128 tokens");
     const size_t p = pos_;
+    const std::pair<int, size_t> key(cur_, n);
     chunk_index_ = 0;
     // Host staging ([position][tokens], one chunk); the previous call has drained, so the
     // pinned buffer is free.
@@ -846,7 +875,7 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     std::memcpy(h_stage_.as<int>() + 1, block, n * 4);
     HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {
-        auto it = graphs_.find(n);
+        auto it = graphs_.find(key);
         if (it == graphs_.end()) {
             hipGraph_t g = nullptr;
             hipGraphExec_t ge = nullptr;
@@ -863,7 +892,7 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
             const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             HIPC(e);
-            it = graphs_.emplace(n, ge).first;
+            it = graphs_.emplace(key, ge).first;
         }
         HIPC(hipGraphLaunch(it->second, stream_));
     } else {
@@ -882,6 +911,113 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     *m = o[0];
     *next = o[1];
     pos_ = p + o[0] + 1;  // truncate(p + m + 1), src/spec.rs:137-139
+}
+
+// Batched verify: one pass over every sequence's block, rows in sequence order. Staging
+// (ints): [attention segments 4 x n_segs][row positions R][row sequences R][block firsts n_seq]
+// [block lengths n_seq][tokens R], moved by one copy.
+void Model::batch_body(const uint32_t* blocks, size_t rows, size_t words, int n_segs) {
+    HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, words * 4, hipMemcpyHostToDevice, stream_));
+    const int* d = stage_.as<int>();
+    BatchView bv;
+    bv.pos = d + 4 * size_t(n_segs);
+    bv.seq = bv.pos + rows;
+    const int* first = bv.seq + rows;
+    const int* len = first + n_seq_;
+    const uint32_t* dtok = reinterpret_cast<const uint32_t*>(len + n_seq_);
+    bv.attn.segs = reinterpret_cast<const int4*>(d);
+    bv.attn.n_segs = n_segs;
+    bv.attn.pos = bv.pos;
+    bv.attn.seq_stride = max_ctx_ * cfg_.kv_dim();
+    stage_pos_ = d;
+    chunk_index_ = 0;
+    forward_chunk(blocks, dtok, rows, rows, false, nullptr, &bv);
+    accept_greedy_batch(amax_.as<uint32_t>(), dtok, first, len, n_seq_, ctl_.as<int>(), bacc_.as<uint32_t>(), stream_);
+    HIPC(hipMemcpyAsync(h_bacc_.p, bacc_.p, (1 + 2 * size_t(n_seq_)) * 4, hipMemcpyDeviceToHost, stream_));
+}
+
+void Model::verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint32_t* m, uint32_t* next) {
+    HIPC(hipSetDevice(device_));
+    if (!blocks || !lens || !m || !next) fail("no blocks, lengths or outputs");
+    seq_pos_[size_t(cur_)] = pos_;
+    size_t rows = 0;
+    for (int q = 0; q < n_seq_; q++) {
+        const std::string who = "sequence " + std::to_string(q);
+        if (lens[q] == 0) fail(who + " has an empty block");
+        if (lens[q] > MAX_BLOCK) fail(who + ": a batched verify block takes at most " + std::to_string(MAX_BLOCK) + " tokens");
+        if (seq_pos_[size_t(q)] + lens[q] > max_ctx_)
+            fail("context is full: " + who + " has " + std::to_string(seq_pos_[size_t(q)]) + " cached + " + std::to_string(lens[q]) +
+                 " new tokens, above the limit of " + std::to_string(max_ctx_));
+        rows += lens[q];
+    }
+    for (size_t i = 0; i < rows; i++)
+        if (blocks[i] >= cfg_.vocab) fail("token id " + std::to_string(blocks[i]) + " is outside the vocabulary");
+    // Attention segments: each sequence's rows cut at 16-row tile boundaries.
+    std::vector<int> segs;
+    for (int q = 0, r = 0; q < n_seq_; q++) {
+        const int end = r + int(lens[q]);
+        while (r < end) {
+            const int e = std::min(end, (r / FTOK + 1) * FTOK);
+            segs.insert(segs.end(), {r, e - r, q, 0});
+            r = e;
+        }
+    }
+    const int n_segs = int(segs.size() / 4);
+    int* hp = h_stage_.as<int>();
+    std::memcpy(hp, segs.data(), segs.size() * 4);
+    int* hpos = hp + segs.size();
+    int* hseq = hpos + rows;
+    int* hfirst = hseq + rows;
+    int* hlen = hfirst + n_seq_;
+    for (int q = 0, r = 0; q < n_seq_; q++) {
+        hfirst[q] = r;
+        hlen[q] = int(lens[q]);
+        for (size_t i = 0; i < lens[q]; i++, r++) {
+            hpos[r] = int(seq_pos_[size_t(q)] + i);
+            hseq[r] = q;
+        }
+    }
+    std::memcpy(hlen + n_seq_, blocks, rows * 4);
+    const size_t words = segs.size() + 3 * rows + 2 * size_t(n_seq_);
+    HIPC(hipEventRecord(ev0_, stream_));
+    if (graphs_on_ && !prof_ && prov_->resident()) {
+        const std::vector<size_t> key(lens, lens + n_seq_);
+        auto it = batch_graphs_.find(key);
+        if (it == batch_graphs_.end()) {
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ge = nullptr;
+            HIPC(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            try {
+                batch_body(blocks, rows, words, n_segs);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream_, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            HIPC(hipStreamEndCapture(stream_, &g));
+            const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            HIPC(e);
+            it = batch_graphs_.emplace(key, ge).first;
+        }
+        HIPC(hipGraphLaunch(it->second, stream_));
+    } else {
+        batch_body(blocks, rows, words, n_segs);
+    }
+    HIPC(hipEventRecord(ev1_, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    harvest();
+    float ms = 0;
+    HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    last_step_ms_ = ms;
+    const uint32_t* o = h_bacc_.as<uint32_t>();
+    check_flow(reinterpret_cast<const int*>(o));  // word 0 is the control block's error word
+    for (int q = 0; q < n_seq_; q++) {
+        m[q] = o[1 + 2 * q];
+        next[q] = o[2 + 2 * q];
+        seq_pos_[size_t(q)] += m[q] + 1;  // truncate(p + m + 1) per sequence, src/spec.rs:137-139
+    }
+    pos_ = seq_pos_[size_t(cur_)];
 }
 
 }  // namespace ls

@@ -95,17 +95,33 @@ public:
 };
 
 std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t compute);
-std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, hipStream_t compute);
+std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, size_t max_rows, hipStream_t compute);
 
+// Device rows of a pass over several sequences (set up by verify_greedy_batch).
+struct BatchView {
+    const int* pos = nullptr;  // per launch row: position in its sequence
+    const int* seq = nullptr;  // per launch row: sequence
+    AttnRows attn;
+};
+
+// One model on one device. It holds n_seq independent sequences (K/V caches and positions)
+// over one copy of the weights; forward, forward_multi, verify_greedy, truncate, reset and pos
+// act on the selected sequence (0 unless select() says otherwise), verify_greedy_batch on all.
 class Model {
 public:
-    Model(const Source& src, int mode, int slots, size_t max_ctx, int device);
+    Model(const Source& src, int mode, int slots, size_t max_ctx, int device, int n_seq = 1);
     ~Model();
     const Config& cfg() const { return cfg_; }
     size_t pos() const { return pos_; }
     size_t max_ctx() const { return max_ctx_; }
     void reset() { pos_ = 0; }
     void truncate(size_t pos);
+    int n_seq() const { return n_seq_; }
+    int selected() const { return cur_; }
+    void select(int seq);
+    // One verify pass over a block per sequence (blocks concatenated, lens[s] tokens for
+    // sequence s): the greedy acceptance of each, as verify_greedy would give it alone.
+    void verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint32_t* m, uint32_t* next);
     // Model::forward: logits/argmax of the last token (each may be null).
     void forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax);
     void forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float* logits, uint32_t* argmax);
@@ -123,12 +139,16 @@ private:
     // logits stored when want_logits.
     // With accept_block (device tokens of a verify block) the argmax kernel also writes the
     // greedy acceptance (m, next) to acc_.
+    // With bv the rows belong to several sequences (positions and caches from bv, no position
+    // update).
     void forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, size_t n_logits, bool want_logits,
-                       const uint32_t* accept_block = nullptr);
+                       const uint32_t* accept_block = nullptr, const BatchView* bv = nullptr);
     const uint32_t* stage_tokens(const uint32_t* tok, size_t n);
     // The device part of a verify step (token and position copies from the pinned staging
     // buffers, forward pass, acceptance, result copy): what a graph captures.
     void verify_body(const uint32_t* block, size_t n);
+    // The device part of a batched verify step; words: staged ints, n_segs: attention segments.
+    void batch_body(const uint32_t* blocks, size_t rows, size_t words, int n_segs);
     void plan_kw_from_env();
     void harvest();
     void prof_begin();
@@ -138,15 +158,17 @@ private:
     Config cfg_;
     int device_;
     size_t max_ctx_, pos_ = 0, chunk_index_ = 0;
+    int n_seq_ = 1, cur_ = 0;
+    std::vector<size_t> seq_pos_;  // positions of the sequences not selected
+    size_t rows_cap_ = 0;          // launch rows the buffers hold (a prefill chunk or a batch)
     hipStream_t stream_ = nullptr;
     std::unique_ptr<DeviceProvider> prov_;
     DevBuf kcache_, vcache_, rope_cos_, rope_sin_, fnorm_, stage_;
     // x_: residual rows; xf_/ss_: fragments and sum-of-squares partials of the next normalised
     // input; af_: attention output fragments; actf_: SiLU(g) * u fragments; part_/cnt_: split-K
     // scratch; hpv_/hpi_: head-block argmax partials; row0_: logits of row 0.
-    DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, ctl_;
-    int attn_splits_ = 1;
-    PinnedBuf h_stage_, h_out_, h_ctl_;
+    DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, ctl_, bacc_;
+    PinnedBuf h_stage_, h_out_, h_ctl_, h_bacc_;
     // Control block: FLOW_WORDS words of fused-launch counters, then the acceptance (m, next).
     static constexpr int CTL_BACK = FLOW_ACC + 2;  // control words copied back after a pass: error, acceptance
     bool fuse_on_ = true;
@@ -160,7 +182,8 @@ private:
     double last_step_ms_ = 0;
     bool prof_ = false;
     bool graphs_on_ = true;
-    std::map<size_t, hipGraphExec_t> graphs_;  // verify step per block length
+    std::map<std::pair<int, size_t>, hipGraphExec_t> graphs_;  // verify step per (sequence, block length)
+    std::map<std::vector<size_t>, hipGraphExec_t> batch_graphs_;  // batched verify step per block lengths
     std::vector<hipEvent_t> prof_ev_;
     size_t prof_used_ = 0;
     ls_kernel_stat prof_acc_{};
