@@ -8,7 +8,13 @@ drafts from a scripted drafter that proposes the target's greedy token with prob
 A step is one fused verify pass (forward over k+1 rows, argmax, acceptance, rollback). W warmup
 steps, then exactly K timed steps. value = verified tokens (m+1 per step) / wall time.
 
-Usage: python bench.py [--gpus 1] [--steps 96] [--warmup 4] [--cpu-steps 24] [--no-cpu]
+--config picks another measurement configuration (same generator and drafter): C1 bf16 weights,
+prompt 64, k=4; C3 int4-g32, prompt 2048 (with --mode stream: weights streamed from pinned host
+memory every pass); C4 16 sequences with their own caches, prompts of U[128,1024] ids, one
+batched verify of 144 rows per step; C5 the Qwen2.5-3B shape, int8-g64, prompt 1024.
+
+Usage: python bench.py [--gpus 1] [--steps 96] [--warmup 4] [--config C2] [--mode resident|stream]
+                       [--cpu-steps N] [--no-cpu]
        python bench.py --calibrate-copy MIB   (one device-to-device copy of MIB MiB, repeated: the
                                                known-size kernel that scales HBM counter readings)
 """
@@ -38,16 +44,13 @@ def hip_sync():
         raise RuntimeError("hipDeviceSynchronize failed")
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "k_mm_qwen05b_int8_verify_hbm_traffic.md")
-
-
-def measured_traffic():
-    """HBM bytes per matrix launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
-    WRITE_SIZE runs of this workload, scaled by a copy of known size), or None."""
+def measured_traffic(path):
+    """HBM bytes per matrix launch from a committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE runs of the workload, scaled by a copy of known size), or None."""
     import re
 
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
         return int(m.group(1)) if m else None
     except OSError:
@@ -82,27 +85,54 @@ def step_bytes(cfg, layer_bytes, row_bytes, ctx, t):
     return L * layer_bytes + cfg["vocab"] * row_bytes + t * row_bytes + 2 * L * kv * 4 * (ctx + t)
 
 
-def build_workload(seed=1, fmt=(8, 64), threads=0):
+# The measurement configurations: C2 is the one the metric is quoted on (the default); the others
+# are the parity cases at their own shapes, measured on request.
+CONFIGS = {
+    "C1": dict(model="0.5b", fmt=(16, 0), prompt=64, k=4, batch=1),
+    "C2": dict(model="0.5b", fmt=(8, 64), prompt=512, k=8, batch=1),
+    "C3": dict(model="0.5b", fmt=(4, 32), prompt=2048, k=8, batch=1),
+    "C4": dict(model="0.5b", fmt=(8, 64), prompt=0, k=8, batch=16),  # prompts of U[128, 1024] ids
+    "C5": dict(model="3b", fmt=(8, 64), prompt=1024, k=8, batch=1),
+}
+FMT_NAME = {16: "bf16", 8: "int8", 4: "int4"}
+
+
+def fmt_tag(fmt):
+    return FMT_NAME[fmt[0]] + (f"-g{fmt[1]}" if fmt[0] != 16 else "")
+
+
+def build_workload(model="0.5b", fmt=(8, 64), seed=1, threads=0):
+    """Random-init N(0, 0.02) weights of the model's shape, bf16, then quantized by the engine's
+    restatement of quant.rs (clip search). Returns (config text of the stored format, parts
+    {layers, embed, norm} of the bf16 model or None, .lsq image or None)."""
     import layerstream_amd as LS
 
-    text = LS.qwen2_config_text(**LS.QWEN2_05B)
+    text = LS.qwen2_config_text(**(LS.QWEN2_05B if model == "0.5b" else LS.QWEN2_3B))
     t0 = time.time()
     m = LS.synth_bf16_model(text, seed, threads=threads)
+    if fmt[0] == 16:
+        log(f"workload: synth {time.time() - t0:.1f}s (bf16)")
+        return text, m, None
     img = LS.quantize_model(text, m["layers"], m["embed"], m["norm"], fmt, clip=True, threads=threads)
+    del m
     log(f"workload: synth + quantize {time.time() - t0:.1f}s, image {img.nbytes / 2**20:.1f} MiB")
-    return text, img
+    return LS.inject_quant(text, *fmt), None, img
 
 
-def cpu_baseline(img, cfg, qtext, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_m):
+def split_parts(img, cfg):
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import tinymodels as T
+
+    return T.split_lsq(img.tobytes(), {"layers": cfg["layers"]})
+
+
+def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_m):
     """The oracle (C restatement of the reference CPU path) on the host's cores: the same prompt
     prefilled, then n_steps verify passes with the same drafts. Returns the JSON object."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_py as O
-    import tinymodels as T
     import layerstream_amd as LS
 
-    parts = T.split_lsq(img.tobytes(), {"layers": cfg["layers"]})
     ocfg = {kk: cfg[kk] for kk in ("format", "embed_format", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "vocab", "eps", "rope_theta")}
     cores = len(os.sched_getaffinity(0))
     om = O.OracleModel(ocfg, parts["layers"], parts["embed"], parts["norm"], threads=cores, max_ctx=len(prompt) + 16 * (n_steps + 2))
@@ -148,15 +178,36 @@ def cpu_baseline(img, cfg, qtext, prompt, drafter_g, p_accept, seed, k, n_steps,
     }
 
 
+def roofline_of(prof, kernel, traffic_path):
+    avg_ms = prof["ms"] / max(prof["launches"], 1)
+    avg_bytes = prof["bytes"] / max(prof["launches"], 1)
+    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": measured_traffic(traffic_path),
+        "traffic_source": os.path.relpath(traffic_path, ROOT) if os.path.exists(traffic_path) else None,
+        "kernel": kernel,
+        "measured_over": f"{ROOF_STEPS} verify steps after the timed ones, start/stop events recorded by each dispatch (hipExtLaunchKernel)",
+        "launches": int(prof["launches"]),
+        "avg_launch_us": round(avg_ms * 1e3, 3),
+        "avg_bytes_per_launch": round(avg_bytes),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=96)
     ap.add_argument("--warmup", type=int, default=4)
-    ap.add_argument("--k", type=int, default=8)
-    ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="C2", help="workload (C2: the headline one)")
+    ap.add_argument("--k", type=int, default=0, help="drafts per step (default: the config's)")
+    ap.add_argument("--ctx", type=int, default=0, help="prompt tokens (default: the config's)")
     ap.add_argument("--p-accept", type=float, default=0.6)
-    ap.add_argument("--cpu-steps", type=int, default=24)
+    ap.add_argument("--cpu-steps", type=int, default=0, help="verify steps timed on the CPU (default 24; 8 for the 3B model)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--mode", choices=["resident", "stream"], default="resident")
     ap.add_argument("--no-graphs", action="store_true", help="launch each kernel of a verify step separately (for tracers)")
@@ -173,22 +224,53 @@ def main():
         calibrate_copy(args.calibrate_copy)
         return
 
+    conf = dict(CONFIGS[args.config])
+    if args.k:
+        conf["k"] = args.k
+    if args.ctx:
+        conf["prompt"] = args.ctx
+    if not args.cpu_steps:
+        args.cpu_steps = 8 if conf["model"] == "3b" else 24
+    if conf["batch"] > 1:
+        run_batch(args, conf)
+    else:
+        run_single(args, conf)
+
+
+def workload_source(conf, mode):
     import layerstream_amd as LS
 
-    qfmt = (8, 64)
-    text, img = build_workload(fmt=qfmt)
-    src = LS.Source.from_lsq_image(img)
-    if args.mode == "stream":
+    text, parts, img = build_workload(conf["model"], conf["fmt"])
+    if img is None:
+        src = LS.Source.from_memory(text, parts["layers"], parts["embed"], parts["norm"])
+    else:
+        src = LS.Source.from_lsq_image(img)
+    if mode == "stream":
         src = src.pinned_copy()
+    return text, parts, img, src
+
+
+def model_tag(conf):
+    return ("qwen05b" if conf["model"] == "0.5b" else "qwen3b") + "_" + FMT_NAME[conf["fmt"][0]]
+
+
+def describe(conf):
+    name = "Qwen2.5-0.5B" if conf["model"] == "0.5b" else "Qwen2.5-3B"
+    return f"{name}-shape {fmt_tag(conf['fmt'])}" + (" (clip search)" if conf["fmt"][0] != 16 else "") + ", random-init N(0,0.02) seed 1"
+
+
+def run_single(args, conf):
+    import layerstream_amd as LS
+
+    text, parts, img, src = workload_source(conf, args.mode)
     cfg = src.config()
-    qtext = LS.inject_quant(text, *qfmt)
-    _, layer_bytes = LS.layer_layout(qtext)
+    _, layer_bytes = LS.layer_layout(text)
     row_bytes = LS.row_bytes(cfg["embed_format"], cfg["hidden"])
-    k, W, K = args.k, args.warmup, args.steps
-    max_new = 9 * (W + K + ROOF_STEPS) + 2
-    max_ctx = args.ctx + max(max_new, args.greedy_ref) + k + 8
+    k, W, K = conf["k"], args.warmup, args.steps
+    max_new = (k + 1) * (W + K + ROOF_STEPS) + 2
+    max_ctx = conf["prompt"] + max(max_new, args.greedy_ref) + k + 8
     rng = np.random.default_rng(512)
-    prompt = rng.integers(0, cfg["vocab"], args.ctx).tolist()
+    prompt = rng.integers(0, cfg["vocab"], conf["prompt"]).tolist()
 
     t0 = time.time()
     model = LS.Model(src, LS.MODE_STREAM if args.mode == "stream" else LS.MODE_RESIDENT, 2, max_ctx)
@@ -205,10 +287,12 @@ def main():
     run = LS.SpecRun(model, drafter, prompt, max_new, k)
     run.step(W)
     hip_sync()
+    rep0 = model.report()
     t0 = time.perf_counter()
     run.step(K)
     hip_sync()
     wall = time.perf_counter() - t0
+    rep1 = model.report()
     # Per-launch timing of the matrix kernels: HIP events on the compute stream around every
     # launch, over ROOF_STEPS further verify steps of the same run (kept out of the timed steps,
     # whose launches they would space out).
@@ -224,28 +308,14 @@ def main():
     out_tokens = run.tokens()
     n_cmp = min(len(out_tokens), len(g))
     match = out_tokens[:n_cmp] == g[:n_cmp]
-    ctx0 = args.ctx + 1 + int(np.sum(m[:W] + 1))
+    ctx0 = conf["prompt"] + 1 + int(np.sum(m[:W] + 1))
     ctx_mean = ctx0 + float(np.mean(np.cumsum(tm + 1) - (tm + 1)))
     sb = step_bytes(cfg, layer_bytes, row_bytes, ctx_mean, k + 1)
     step_ms_p50 = float(np.median(tms))
-
-    avg_ms = prof["ms"] / max(prof["launches"], 1)
-    avg_bytes = prof["bytes"] / max(prof["launches"], 1)
-    achieved = avg_bytes / (avg_ms * 1e-3) / 1e9 if avg_ms > 0 else 0.0
-    roofline = {
-        "bound": "hbm",
-        "achieved": round(achieved, 1),
-        "peak": HBM_PEAK_GBS,
-        "unit": "GB/s",
-        "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": measured_traffic(),
-        "traffic_source": os.path.relpath(TRAFFIC_PROFILE, ROOT),
-        "kernel": "k_mm (fused MFMA weight-streaming matmul: q|k|v, o, gate|up, down, head; int8, t=9)",
-        "measured_over": f"{ROOF_STEPS} verify steps after the timed ones, start/stop events recorded by each dispatch (hipExtLaunchKernel)",
-        "launches": int(prof["launches"]),
-        "avg_launch_us": round(avg_ms * 1e3, 3),
-        "avg_bytes_per_launch": round(avg_bytes),
-    }
+    tag = model_tag(conf)
+    traffic_path = os.path.join(ROOT, "profiles", f"k_mm_{tag}_verify_hbm_traffic.md")
+    roofline = roofline_of(prof, f"k_mm (fused MFMA weight-streaming matmul: q|k|v, o, gate|up, down, head; {FMT_NAME[conf['fmt'][0]]}, t={k + 1})",
+                           traffic_path)
     res = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -260,7 +330,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": "Qwen2.5-0.5B-shape int8-g64 (clip search), random-init N(0,0.02) seed 1; prompt 512 random ids; k=8 chain drafts, scripted 60% per-token acceptance; greedy verify",
+            "workload": f"{args.config}: {describe(conf)}; prompt {conf['prompt']} random ids; k={k} chain drafts, scripted "
+            f"{round(100 * args.p_accept)}% per-token acceptance; greedy verify",
             "mode": args.mode,
             "k": k,
             "ctx_start": ctx0,
@@ -277,12 +348,157 @@ def main():
         "roofline": roofline,
         "cpu_baseline": None,
     }
+    if args.mode == "stream":
+        h2d = rep1["h2d_bytes"] - rep0["h2d_bytes"]
+        res["stream"] = {
+            "h2d_bytes_per_step": int(h2d / K),
+            "h2d_GBps": round(h2d / wall / 1e9, 2),
+            "host_wait_ms_per_step": round((rep1["wait_ns"] - rep0["wait_ns"]) / K / 1e6, 4),
+            "note": "weights cross PCIe from pinned host memory every pass (2 device slots)",
+        }
     if not args.no_cpu:
         t0 = time.time()
-        res["cpu_baseline"] = cpu_baseline(img, cfg, qtext, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m))
+        cparts = parts if img is None else split_parts(img, cfg)
+        res["cpu_baseline"] = cpu_baseline(cparts, cfg, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m))
         log(f"cpu baseline {time.time() - t0:.1f}s")
     run.close()
     drafter.close()
+    print(json.dumps(res), flush=True)
+
+
+def run_batch(args, conf):
+    """C4: n sequences with their own caches, prompts of U[128, 1024] ids (seeded), k drafts
+    each from a scripted drafter per sequence; one batched verify pass per step. Parity: every
+    sequence's emitted tokens equal its own greedy continuation."""
+    import layerstream_amd as LS
+
+    text, parts, img, src = workload_source(conf, args.mode)
+    cfg = src.config()
+    _, layer_bytes = LS.layer_layout(text)
+    row_bytes = LS.row_bytes(cfg["embed_format"], cfg["hidden"])
+    n, k, W, K = conf["batch"], conf["k"], args.warmup, args.steps
+    V = cfg["vocab"]
+    rng = np.random.default_rng(512)
+    lens = rng.integers(128, 1025, n)
+    prompts = [rng.integers(0, V, int(L)).tolist() for L in lens]
+    steps_all = W + K + ROOF_STEPS
+    # Greedy tokens scripting each drafter: ~2.5 tokens are emitted per step at 60%; beyond the
+    # script the drafter proposes other tokens (parity is checked over the scripted part).
+    g_len = min((k + 1) * steps_all + 2, 4 * steps_all + 64)
+    max_ctx = int(lens.max()) + g_len + k + 8
+    mode = LS.MODE_STREAM if args.mode == "stream" else LS.MODE_RESIDENT
+
+    # Each sequence's greedy continuation, from a one-sequence model (the reference's setup).
+    t0 = time.time()
+    alone = LS.Model(src, mode, 2, max_ctx)
+    greedy = []
+    for p in prompts:
+        alone.reset()
+        greedy.append(LS.greedy_generate(alone, p, g_len))
+    alone.close()
+    log(f"greedy references {n} x {g_len} tokens in {time.time() - t0:.1f}s")
+
+    t0 = time.time()
+    model = LS.Model(src, mode, 2, max_ctx, 0, n_seq=n)
+    if args.no_graphs:
+        model.use_graphs(False)
+    outs, last = [], []
+    for s, p in enumerate(prompts):
+        model.select(s)
+        a = model.forward_argmax(p)
+        outs.append([a])
+        last.append(a)
+    log(f"batch model load + {n} prompts {time.time() - t0:.1f}s")
+    drafters = [LS.ScriptedDrafter(greedy[s], args.p_accept, 2024 + s, V) for s in range(n)]
+    step_ms, step_tok, ctx_log = [], [], []
+
+    def step():
+        blocks = []
+        for s in range(n):
+            blocks.append([last[s]] + [drafters[s].token(len(outs[s]) + i) for i in range(k)])
+        ctx_log.append(sum(len(p) + len(o) for p, o in zip(prompts, outs)))
+        res = model.verify_greedy_batch(blocks)
+        got = 0
+        for s, (mm, nx) in enumerate(res):
+            outs[s].extend(blocks[s][1 : 1 + mm] + [nx])
+            last[s] = nx
+            got += mm + 1
+        step_ms.append(model.last_step_ms())
+        step_tok.append(got)
+
+    for _ in range(W):
+        step()
+    hip_sync()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        step()
+    hip_sync()
+    wall = time.perf_counter() - t0
+    model.profile(True)
+    for _ in range(ROOF_STEPS):
+        step()
+    hip_sync()
+    prof = model.profile_read()
+    model.profile(False)
+    match = all(o[: min(len(o), len(g))] == g[: min(len(o), len(g))] for o, g in zip(outs, greedy))
+    toks = int(np.sum(step_tok[W : W + K]))
+    tms = np.array(step_ms[W : W + K])
+    ctx_sum = float(np.mean(ctx_log[W : W + K]))
+    # bytes: every layer block and the head once, t embedding rows, and every sequence's cache
+    L, kvd = cfg["layers"], cfg["kv_heads"] * cfg["head_dim"]
+    t = n * (k + 1)
+    sb = L * layer_bytes + V * row_bytes + t * row_bytes + 2 * L * kvd * 4 * (ctx_sum + t)
+    h, inter, hq = cfg["hidden"], cfg["inter"], cfg["heads"] * cfg["head_dim"]
+    params = L * (h * (hq + 2 * kvd) + hq * h + 3 * h * inter) + V * h
+    flops = 2 * t * params + 4 * L * cfg["heads"] * cfg["head_dim"] * (k + 1) * ctx_sum
+    p50 = float(np.median(tms))
+    traffic_path = os.path.join(ROOT, "profiles", f"k_mm_{model_tag(conf)}_batch{n}_verify_hbm_traffic.md")
+    res = {
+        "metric": METRIC,
+        "value": round(toks / wall, 2),
+        "unit": "verified tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.config}: {describe(conf)}; {n} sequences, prompts of U[128,1024] random ids; k={k} chain drafts each, "
+            f"scripted {round(100 * args.p_accept)}% per-token acceptance; one batched verify of {t} rows per step",
+            "mode": args.mode,
+            "k": k,
+            "sequences": n,
+            "rows_per_step": t,
+            "ctx_mean_per_sequence": round(ctx_sum / n, 1),
+            "graphs": not args.no_graphs,
+        },
+        "verify_ms_p50": round(p50, 4),
+        "verify_ms_p90": round(float(np.percentile(tms, 90)), 4),
+        "tokens_per_step": round(toks / K, 3),
+        "step_algorithmic_bytes": int(sb),
+        "step_hbm_frac": round(sb / (p50 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "step_tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
+        "step_mfma_frac_bf16_dense": round(flops / (p50 * 1e-3) / 2.5e15, 4),
+        "tokens_match_greedy": bool(match),
+        "roofline": roofline_of(prof, f"k_mm (fused MFMA weight-streaming matmul; {FMT_NAME[conf['fmt'][0]]}, t={t})", traffic_path),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        # The reference verifies one sequence at a time (one cache per Model): its batch rate is
+        # its single-sequence rate. Timed on sequence 0's prompt and drafts.
+        t0 = time.time()
+        cparts = parts if img is None else split_parts(img, cfg)
+        cb = cpu_baseline(cparts, cfg, prompts[0], greedy[0], args.p_accept, 2024, k, args.cpu_steps, [])
+        cb["sample"] = "sequence 0 only (the reference runs sequences one after another); " + cb["sample"]
+        cb.pop("accepted_match_gpu", None)
+        res["cpu_baseline"] = cb
+        log(f"cpu baseline {time.time() - t0:.1f}s")
+    for d in drafters:
+        d.close()
     print(json.dumps(res), flush=True)
 
 
