@@ -72,58 +72,94 @@ __device__ __forceinline__ uint32_t raw_elem(const uint8_t* row, int bits, int g
     return wj < half ? (b & 15u) : (b >> 4);
 }
 
-// One thread per (row, chunk): the 64 bytes of its four lane slots.
-__global__ void k_tile_repack(const uint8_t* __restrict__ raw, int rows, TMat m, int row_off, int block, int stride,
-                              int pair_hd) {
-    const int r = blockIdx.x;
+// One wavefront per source row: the row (reference layout: data, then the bf16 group scales) is
+// staged in LDS with coalesced loads; then each lane assembles whole 16-byte lane slots of the
+// tile layout (chunk c, lane group lg: columns 32 q + 8 lg + [0, 8) of every k-step q of the
+// chunk) and stores each with one 16-byte store; the scales go to [strip][group][16 rows].
+// Padding columns get zero weights (int4: nibble 8).
+template <int BITS>
+__global__ __launch_bounds__(256) void k_tile_repack(const uint8_t* __restrict__ raw, int rows, TMat m, int row_off, int block,
+                                                     int stride, int pair_hd, int rpw, int lds_row) {
+    extern __shared__ __align__(16) float lds_f[];
+    uint8_t* lds = reinterpret_cast<uint8_t*>(lds_f);
+    constexpr int CC = BITS == 16 ? 32 : (BITS == 8 ? 64 : 128), Q = CC / 32;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = blockIdx.x * rpw + w;
+    const int K = m.cols;
+    const int db = BITS == 16 ? 2 * K : K * BITS / 8;
+    const int ng_real = BITS == 16 ? 0 : K / m.group;
+    const int rb = db + 2 * ng_real;
+    uint8_t* L = lds + size_t(w) * lds_row;
+    if (r < rows) {
+        const uint8_t* row = raw + size_t(r) * rb;
+        if (((reinterpret_cast<uintptr_t>(row) | uintptr_t(rb)) & 3) == 0) {
+            const uint32_t* r4 = reinterpret_cast<const uint32_t*>(row);
+            uint32_t* l4 = reinterpret_cast<uint32_t*>(L);
+            for (int i = lane; i < rb / 4; i += 64) l4[i] = r4[i];
+        } else {
+            for (int i = lane; i < rb; i += 64) L[i] = row[i];
+        }
+    }
+    __syncthreads();
     if (r >= rows) return;
-    const int bits = m.bits, K = m.cols;
-    const int db = bits == 16 ? 2 * K : K * bits / 8;
-    const int ng_real = bits == 16 ? 0 : K / m.group;
-    const uint8_t* row = raw + size_t(r) * (db + 2 * ng_real);
     int lr = r;
     if (pair_hd > 0) {
         const int d = r % pair_hd, half = pair_hd / 2;
         lr = r - d + (d < half ? 2 * d : 2 * (d - half) + 1);
     }
     const int dr = row_off + (lr / block) * stride + lr % block, strip = dr / 16, rl = dr % 16;
-    const int cc = tile_chunk_cols(bits), Q = cc / 32;
     uint8_t* data = const_cast<uint8_t*>(m.data);
-    for (int c = threadIdx.x; c < m.n_chunks; c += blockDim.x) {
-        for (int lg = 0; lg < 4; lg++) {
-            uint8_t out[16];
-            for (int i = 0; i < 16; i++) out[i] = bits == 4 ? 0x88 : 0;
-            for (int q = 0; q < Q; q++)
-                for (int j = 0; j < 8; j++) {
-                    const int col = c * cc + 32 * q + 8 * lg + j;
-                    if (col >= K) continue;
-                    const uint32_t v = raw_elem(row, bits, m.group, col);
-                    if (bits == 16) {
-                        out[2 * j] = uint8_t(v);
-                        out[2 * j + 1] = uint8_t(v >> 8);
-                    } else if (bits == 8) {
-                        out[8 * q + j] = uint8_t(v);
-                    } else {
-                        uint8_t& o = out[4 * q + j / 2];
-                        o = (j & 1) ? uint8_t((o & 0x0f) | (v << 4)) : uint8_t((o & 0xf0) | v);
-                    }
+    for (int p = lane; p < m.n_chunks * 4; p += 64) {
+        const int c = p >> 2, lg = p & 3;
+        uint8_t out[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) out[i] = BITS == 4 ? 0x88 : 0;
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int col = c * CC + 32 * q + 8 * lg + j;
+                if (col >= K) continue;
+                const uint32_t v = raw_elem(L, BITS, m.group, col);
+                if constexpr (BITS == 16) {
+                    out[2 * j] = uint8_t(v);
+                    out[2 * j + 1] = uint8_t(v >> 8);
+                } else if constexpr (BITS == 8) {
+                    out[8 * q + j] = uint8_t(v);
+                } else {
+                    uint8_t& o = out[4 * q + j / 2];
+                    o = (j & 1) ? uint8_t((o & 0x0f) | (v << 4)) : uint8_t((o & 0xf0) | v);
                 }
-            uint8_t* dst = data + ((size_t(strip) * m.n_chunks + c) * 64 + rl + 16 * lg) * 16;
-            for (int i = 0; i < 16; i++) dst[i] = out[i];
-        }
+            }
+        uint4 o4;
+        __builtin_memcpy(&o4, out, 16);
+        *reinterpret_cast<uint4*>(data + ((size_t(strip) * m.n_chunks + c) * 64 + rl + 16 * lg) * 16) = o4;
     }
-    if (bits != 16) {
+    if (BITS != 16) {
         uint16_t* sc = const_cast<uint16_t*>(m.scales);
-        for (int g = threadIdx.x; g < ng_real; g += blockDim.x)
-            sc[(size_t(strip) * m.n_groups + g) * 16 + rl] = uint16_t(row[db + 2 * g] | (row[db + 2 * g + 1] << 8));
+        for (int g = lane; g < ng_real; g += 64)
+            sc[(size_t(strip) * m.n_groups + g) * 16 + rl] = uint16_t(L[db + 2 * g] | (L[db + 2 * g + 1] << 8));
     }
 }
+
+constexpr size_t REPACK_LDS = 64 * 1024;  // LDS of one repack workgroup (up to 4 rows)
 
 void tile_repack(const uint8_t* raw, int rows, const TMat& dst, int row_off, int block, int stride, hipStream_t s,
                  int pair_hd) {
     if (rows <= 0) return;
     if (pair_hd > 0 && (pair_hd % 2 || rows % pair_hd)) throw std::runtime_error("RoPE pairing needs whole even heads");
-    hipLaunchKernelGGL(k_tile_repack, dim3(rows), dim3(64), 0, s, raw, rows, dst, row_off, block, stride, pair_hd);
+    const int K = dst.cols;
+    const size_t rb = dst.bits == 16 ? 2 * size_t(K) : size_t(K) * dst.bits / 8 + 2 * size_t(K / dst.group);
+    const size_t lds_row = (rb + 15) / 16 * 16;
+    if (lds_row > REPACK_LDS) throw std::runtime_error("row too long for the repack kernel");
+    const int rpw = int(std::min<size_t>(4, REPACK_LDS / lds_row));
+    const dim3 grid((rows + rpw - 1) / rpw), blk(64 * rpw);
+    const size_t lds = size_t(rpw) * lds_row;
+    switch (dst.bits) {
+        case 16: hipLaunchKernelGGL(k_tile_repack<16>, grid, blk, lds, s, raw, rows, dst, row_off, block, stride, pair_hd, rpw, int(lds_row)); break;
+        case 8: hipLaunchKernelGGL(k_tile_repack<8>, grid, blk, lds, s, raw, rows, dst, row_off, block, stride, pair_hd, rpw, int(lds_row)); break;
+        default: hipLaunchKernelGGL(k_tile_repack<4>, grid, blk, lds, s, raw, rows, dst, row_off, block, stride, pair_hd, rpw, int(lds_row)); break;
+    }
     FCHECK(hipGetLastError());
 }
 

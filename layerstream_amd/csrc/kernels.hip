@@ -2,6 +2,7 @@
 // embedding helpers of streamed tables. The weight-streaming kernels live in fused.hip.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
@@ -328,6 +329,21 @@ __global__ void k_bf16_to_f32(const uint8_t* __restrict__ src, int n, float* __r
 
 void bf16_to_f32_dev(const uint8_t* src, int n, float* dst, hipStream_t s) {
     hipLaunchKernelGGL(k_bf16_to_f32, dim3((n + 255) / 256), dim3(256), 0, s, src, n, dst);
+    HIPCHECK(hipGetLastError());
+}
+
+// Vector blockIdx.y of w, 256 elements per workgroup along x.
+__global__ void k_bf16_to_f32_multi(Widen w) {
+    const int v = blockIdx.y, i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < w.n[v]) w.dst[v][i] = __uint_as_float(uint32_t(w.src[v][2 * i] | (w.src[v][2 * i + 1] << 8)) << 16);
+}
+
+void bf16_to_f32_dev(const Widen& w, hipStream_t s) {
+    if (w.count <= 0) return;
+    if (w.count > Widen::MAX) throw std::runtime_error("too many vectors for one widening launch");
+    int n = 0;
+    for (int v = 0; v < w.count; v++) n = std::max(n, w.n[v]);
+    hipLaunchKernelGGL(k_bf16_to_f32_multi, dim3((n + 255) / 256, w.count), dim3(256), 0, s, w);
     HIPCHECK(hipGetLastError());
 }
 

@@ -31,6 +31,21 @@ void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, 
                const float* k_cache, const float* v_cache, float* scratch, int* cnt, uint8_t* frags, hipStream_t s);
 // dst[i] = widened bf16 src[i] (little-endian bytes), i < n.
 void bf16_to_f32_dev(const uint8_t* src, int n, float* dst, hipStream_t s);
+// Several such vectors in one launch.
+struct Widen {
+    static constexpr int MAX = 8;
+    const uint8_t* src[MAX] = {};
+    float* dst[MAX] = {};
+    int n[MAX] = {};
+    int count = 0;
+    void add(const uint8_t* s, int len, float* d) {
+        src[count] = s;
+        n[count] = len;
+        dst[count] = d;
+        count++;
+    }
+};
+void bf16_to_f32_dev(const Widen& w, hipStream_t s);
 // x[t][cols] = dequantized raw embedding rows raw[t][row_bytes] (reference row layout).
 void embed_raw_rows(const uint8_t* raw, int bits, int group, int cols, int t, float* x, hipStream_t s);
 

@@ -125,11 +125,13 @@ void build_layer_device(const Config& c, const LayerLayout& L, const uint8_t* ra
     tile_repack(raw + L.off[T_UP], in, D.gu, gb, gb, 2 * gb, s);
     tile_repack(raw + L.off[T_DOWN], h, D.down, 0, h, h, s);
     float* bq = reinterpret_cast<float*>(b + a.b_qkv);
-    bf16_to_f32_dev(raw + L.off[T_Q_B], h, bq, s);
-    bf16_to_f32_dev(raw + L.off[T_K_B], kv, bq + h, s);
-    bf16_to_f32_dev(raw + L.off[T_V_B], kv, bq + h + kv, s);
-    bf16_to_f32_dev(raw + L.off[T_INPUT_NORM], h, reinterpret_cast<float*>(b + a.in_norm), s);
-    bf16_to_f32_dev(raw + L.off[T_POST_NORM], h, reinterpret_cast<float*>(b + a.post_norm), s);
+    Widen w;
+    w.add(raw + L.off[T_Q_B], h, bq);
+    w.add(raw + L.off[T_K_B], kv, bq + h);
+    w.add(raw + L.off[T_V_B], kv, bq + h + kv);
+    w.add(raw + L.off[T_INPUT_NORM], h, reinterpret_cast<float*>(b + a.in_norm));
+    w.add(raw + L.off[T_POST_NORM], h, reinterpret_cast<float*>(b + a.post_norm));
+    bf16_to_f32_dev(w, s);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -205,9 +207,11 @@ private:
 
 // ---------------------------------------------------------------------------------------
 // Streaming: `slots` device slots fed in schedule order (StreamProvider, src/provider.rs:161-352).
-// A slot holds the raw block (copied host -> device on a side stream), the arena it is
-// rearranged into, and events: `copied` (its host staging buffer may be refilled), `ready`
-// (the arena may be computed on) and `freed` (the compute stream is done with it). With a
+// A slot holds the raw block (copied host -> device on a copy stream), the arena it is
+// rearranged into (on a build stream, so one item's rearrangement overlaps the next one's
+// copy), and events: `copied` (its host staging buffer may be refilled), `ready` (the arena
+// may be computed on and the raw buffer refilled) and `freed` (the compute stream is done with
+// the arena). With a
 // pinned source the copy goes straight from the source's memory; otherwise the host reads
 // into a pinned staging buffer first.
 // ---------------------------------------------------------------------------------------
@@ -230,6 +234,7 @@ public:
         : src_(src), c_(src.cfg()), L_(src.layout()), a_(layer_arena(c_)), compute_(compute), max_rows_(max_rows) {
         if (slots < 1) slots = 1;
         HIPC(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking));
+        HIPC(hipStreamCreateWithFlags(&build_, hipStreamNonBlocking));
         const size_t rb = c_.row_bytes();
         buf_size_ = std::max(L_.total, std::min(HEAD_ROWS, c_.vocab) * rb);
         const Format ef = c_.embed_format;
@@ -254,6 +259,7 @@ public:
     }
     ~StreamProvider() override {
         (void)hipStreamSynchronize(copy_);
+        (void)hipStreamSynchronize(build_);
         (void)hipStreamSynchronize(compute_);
         for (auto& s : slots_) {
             (void)hipEventDestroy(s.copied);
@@ -261,6 +267,7 @@ public:
             (void)hipEventDestroy(s.freed);
         }
         (void)hipEventDestroy(embed_copied_);
+        (void)hipStreamDestroy(build_);
         (void)hipStreamDestroy(copy_);
     }
     const char* name() const override { return "stream"; }
@@ -268,6 +275,7 @@ public:
     void begin_forward(bool with_head) override {
         // Recover from an earlier pass that stopped early: wait for copies in flight.
         HIPC(hipStreamSynchronize(copy_));
+        HIPC(hipStreamSynchronize(build_));
         schedule_.clear();
         for (size_t l = 0; l < c_.layers; l++) schedule_.push_back({LAYER, l});
         if (with_head)
@@ -345,17 +353,23 @@ private:
             else src_.read_embed_rows(first, rows, s.stage.as<uint8_t>());
             from = s.stage.as<uint8_t>();
         }
-        if (s.used) HIPC(hipStreamWaitEvent(copy_, s.freed, 0));
+        // The raw buffer is free once the previous item's build has read it; the arena once the
+        // compute stream is done with that item. The copy waits only for the former.
+        if (s.used) HIPC(hipStreamWaitEvent(copy_, s.ready, 0));
         HIPC(hipMemcpyAsync(s.raw.p, from, bytes, hipMemcpyHostToDevice, copy_));
         h2d_bytes_ += bytes;
         HIPC(hipEventRecord(s.copied, copy_));
+        // The tile layout is built on a stream of its own, so the next item's PCIe copy runs
+        // meanwhile.
+        HIPC(hipStreamWaitEvent(build_, s.copied, 0));
+        if (s.used) HIPC(hipStreamWaitEvent(build_, s.freed, 0));
         if (it.kind == LAYER) {
-            build_layer_device(c_, L_, s.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), copy_);
+            build_layer_device(c_, L_, s.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), build_);
         } else {
             TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
-            tile_repack(s.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), copy_);
+            tile_repack(s.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), build_);
         }
-        HIPC(hipEventRecord(s.ready, copy_));
+        HIPC(hipEventRecord(s.ready, build_));
         s.used = true;
         next_issue_++;
     }
@@ -386,7 +400,7 @@ private:
     LayerLayout L_;
     LayerArena a_;
     TMat hshape_;
-    hipStream_t compute_, copy_ = nullptr;
+    hipStream_t compute_, copy_ = nullptr, build_ = nullptr;
     std::vector<Slot> slots_;
     std::vector<Item> schedule_;
     size_t next_issue_ = 0, next_take_ = 0, buf_size_ = 0;
