@@ -368,11 +368,27 @@ enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_HEAD = 3 };
 // 1 / rms per token of a tile from the producer's sum-of-squares partials, by one wavefront:
 // lane (part, token) adds slots part, part + 4, ... in order (loads issued 16 at a time), then a
 // fixed shuffle tree over the four parts (src/kernels.rs:217-228 up to the summation order).
-__device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, float* inv) {
+// The first 16 loads are issued by rms_issue (at workgroup entry, beside the weight loads) and
+// consumed by rms_finish (after the matrix work), so their latency hides behind the weights'.
+struct RmsLoads {
+    float x[16];
+};
+__device__ __forceinline__ void rms_issue(const MMArgs& a, int tile, RmsLoads& r) {
+    const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
+    const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const int sl = part + 4 * k;
+        r.x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
+    }
+}
+__device__ __forceinline__ void rms_finish(const MMArgs& a, int tile, int cols, const RmsLoads& r, float* inv) {
     const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
     const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
     float v = 0.0f;
-    for (int k0 = 0; part + 4 * k0 < a.ss_slots; k0 += 16) {
+#pragma unroll
+    for (int k = 0; k < 16; k++) v += r.x[k];
+    for (int k0 = 16; part + 4 * k0 < a.ss_slots; k0 += 16) {
         float x[16];
 #pragma unroll
         for (int k = 0; k < 16; k++) {
@@ -385,6 +401,11 @@ __device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, flo
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     if (lane < FTOK) inv[lane] = 1.0f / sqrtf(v / float(cols) + a.eps);
+}
+__device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, float* inv) {
+    RmsLoads r;
+    rms_issue(a, tile, r);
+    rms_finish(a, tile, cols, r, inv);
 }
 
 __device__ __forceinline__ bool beats(float va, int ia, float vb, int ib) {
@@ -507,6 +528,10 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             }
         }
     }
+    // Sum-of-squares partials for 1 / rms (wavefront 0), in flight with the weights.
+    RmsLoads rms;
+    const bool do_rms = a.ss && wv == 0;
+    if (do_rms) rms_issue(a, tile, rms);
     // Epilogue operands, staged in LDS while the weights are in flight.
     if constexpr (EPI == EPI_RESID) {
         for (int e0 = threadIdx.x; e0 < rows_wg * FTOK; e0 += 4 * nthr) {
@@ -540,7 +565,6 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             rsin[tok * half + j] = a.rope_sin[at];
         }
     }
-    if (a.ss && wv == 0) inv_rms(a, tile, W.cols, inv);
     if constexpr (IN_FLOW) {
         // The weights are in flight; wait for the input, then read it coherently.
         flow_wait(fl, sp);
@@ -568,6 +592,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
 #pragma unroll
     for (int c = 0; c < CPW; c++)
         if (c < nch) chunk_mfma<BITS, G16, S>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
+    if (do_rms) rms_finish(a, tile, W.cols, rms, inv);  // read after the barrier below
 
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
     // rows 16 r + 4 (l / 16) + i of token l % 16.
@@ -693,17 +718,18 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             }
         }
     } else if constexpr (EPI == EPI_SILU) {
-        // rows: [16 S gate rows | 16 S up rows] for act columns 16 S rb + [0, 16 S)
+        // rows: [h gate rows | h up rows] for act columns h rb + [0, h), h = rows_wg / 2
+        const int hw = rows_wg / 2;
         uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
         const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(a.ofrag_stride), BUF_DWORD3);
-        for (int q = threadIdx.x; q < (2 * S) * FTOK; q += nthr) {
-            const int cg = q / FTOK, tok = q % FTOK, col = 16 * S * rb + 8 * cg;
+        for (int q = threadIdx.x; q < (hw / 8) * FTOK; q += nthr) {
+            const int cg = q / FTOK, tok = q % FTOK, col = hw * rb + 8 * cg;
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 v[j] = 0.0f;
                 if (tok < nt) {
-                    float g = tl[(8 * cg + j) * FTOK + tok], up = tl[(16 * S + 8 * cg + j) * FTOK + tok];
+                    float g = tl[(8 * cg + j) * FTOK + tok], up = tl[(hw + 8 * cg + j) * FTOK + tok];
                     if (a.ss) {
                         g = __fmul_rn(g, inv[tok]);
                         up = __fmul_rn(up, inv[tok]);
@@ -779,7 +805,7 @@ __global__ __launch_bounds__(1024) void k_gu_down(MMArgs gu, MMPlan pgu, MMArgs 
     const int ngu = pgu.nrb * pgu.nsplit;
     if (int(blockIdx.x) < ngu) {
         if (int(threadIdx.x) >= 64 * pgu.rg * pgu.kw) return;
-        mm_body<BITS, EPI_SILU, G16, GU_STRIPS, false, true>(gu, pgu, sc, fl, blockIdx.x, 0, smem);
+        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), false, true>(gu, pgu, sc, fl, blockIdx.x, 0, smem);
     } else {
         if (int(threadIdx.x) >= 64 * pdn.rg * pdn.kw) return;
         mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, false>(dn, pdn, sc, fl, blockIdx.x - ngu, 0, smem);
@@ -957,6 +983,11 @@ MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
     return p;
 }
 
+MMPlan gu_plan(const TMat& W, int kw, int n_tokens) {
+    const int gs = gu_wave_strips(W.bits, W.group);
+    return mm_plan(W, 2 * GU_STRIPS / gs, kw, n_tokens, gs);
+}
+
 size_t mm_part_floats(const MMPlan& p) {
     return p.nsplit > 1 ? size_t(p.tiles) * p.nrb * p.nsplit * 16 * p.s * p.rg * FTOK : 0;
 }
@@ -1020,13 +1051,16 @@ void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStrea
     }
 }
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
-    if (p.rg != 2) throw std::runtime_error("gate|up runs gate and up row blocks together");
-    launch<EPI_SILU, GU_STRIPS>(a, p, sc, s);
+    const int gs = gu_wave_strips(a.W.bits, a.W.group);
+    if (p.s != gs || p.s * p.rg != 2 * GU_STRIPS) throw std::runtime_error("gate|up plan does not hold a gate block and its up block");
+    if (gs == 2 * GU_STRIPS) launch<EPI_SILU, 2 * GU_STRIPS>(a, p, sc, s);
+    else launch<EPI_SILU, GU_STRIPS>(a, p, sc, s);
 }
 
 void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, const MMPlan& pdn, const MMScratch& sc,
                      int* ctl, hipStream_t s) {
-    if (pgu.rg != 2 || pgu.s != GU_STRIPS || pdn.s != DOWN_STRIPS) throw std::runtime_error("gate|up/down plans do not match");
+    if (pgu.s != gu_wave_strips(gu.W.bits, gu.W.group) || pgu.s * pgu.rg != 2 * GU_STRIPS || pdn.s != DOWN_STRIPS)
+        throw std::runtime_error("gate|up/down plans do not match");
     if (pgu.tiles != 1 || pdn.tiles != 1) throw std::runtime_error("the fused gate|up/down launch takes one token tile");
     if (pgu.nsplit != 1) throw std::runtime_error("the fused gate|up/down launch needs gate|up without a K split");
     if (pdn.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");

@@ -56,8 +56,13 @@ void tile_clear(const TMat& m, hipStream_t s);
 __host__ __device__ inline size_t frag_tile_bytes(int cols) { return size_t(tile_kpad(cols)) / 32 * 3 * 1024; }
 // Sum-of-squares slots (16 columns each) of a row of `cols` values.
 __host__ __device__ inline int ss_slots(int cols) { return (cols + 15) / 16; }
-// gate|up rows are interleaved in blocks of 16 * GU_STRIPS (gate block, up block, ...).
+// gate|up rows are interleaved in blocks of 16 * GU_STRIPS (gate block, up block, ...). A
+// workgroup row group holds a gate block and its up block: for int8 and int4 with groups of 32+
+// one wavefront streams both (4 strips), so the input fragments it loads serve both; bf16 and
+// groups of 16 need the registers for their wider chunks or extra MFMAs, and use two wavefronts
+// of one block each.
 constexpr int GU_STRIPS = 2;
+__host__ __device__ constexpr int gu_wave_strips(int bits, int group) { return (bits == 16 || group == 16) ? GU_STRIPS : 2 * GU_STRIPS; }
 // Strips per wavefront of the down projection: its K (the FFN width) is long and its rows few,
 // so two strips halve the input-fragment reads per weight byte.
 constexpr int DOWN_STRIPS = 2;
@@ -117,6 +122,8 @@ struct MMPlan {
     int s = 1, rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
 };
 MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips);
+// The gate|up plan: gu_wave_strips strips per wavefront, row groups making one gate and up block.
+MMPlan gu_plan(const TMat& W, int kw, int n_tokens);
 size_t mm_part_floats(const MMPlan& p);
 size_t mm_counters(const MMPlan& p);
 
@@ -153,8 +160,8 @@ void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
 // x[row] += W x; then fragments of x * onorm and sum-of-squares partials of the new rows (plan
 // strips 1, 2 or 4).
 void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
-// gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan strips GU_STRIPS,
-// rg 2) + 1/rms + SiLU(g) * u -> act fragments.
+// gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan from gu_plan) +
+// 1/rms + SiLU(g) * u -> act fragments.
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // gate|up then down (plan strips DOWN_STRIPS) in one launch for one token tile: each down K
 // split waits only for the gate|up row blocks that produce its columns. ctl is the control

@@ -509,7 +509,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const int n = int(T);
         const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(HEAD_ROWS), int(h), 256);
         const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1),        mm_plan(la.o, 1, kw_o_, n, 1),
-                                mm_plan(la.gu, 2, kw_gu_, n, GU_STRIPS), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS),
+                                gu_plan(la.gu, kw_gu_, n), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS),
                                 mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};
         size_t pf = 0, nc = 0;
         for (const MMPlan& pl : plans) {
@@ -757,7 +757,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 d.oss = ss;
                 d.oss_slots = slots_h_;
             }
-            const MMPlan pg = mm_plan(L.gu, 2, kw_gu_, T, GU_STRIPS), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS);
+            const MMPlan pg = gu_plan(L.gu, kw_gu_, T), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS);
             // Fused only when both roles fit on the device at one workgroup per CU (their
             // wavefronts fill a CU's register file): a down workgroup that started after a
             // gate|up one had finished would fetch its weights late. Either path gives the same
