@@ -22,25 +22,28 @@ namespace ls {
     } while (0)
 
 // ---------------------------------------------------------------------------------------
-// Causal GQA attention (src/model.rs:261-282), flash-decoding over chunks of ACH keys. The
-// reference computes scores (q . k_j) * scale, a softmax (max, exp(x - max), sum, * 1/sum) and
-// sum_j p_j v_j over every cached position.
+// Causal GQA attention (src/model.rs:261-282), flash-decoding. The reference computes scores
+// (q . k_j) * scale, a softmax (max, exp(x - max), sum, * 1/sum) and sum_j p_j v_j over every
+// cached position.
 //
-// One launch: grid (ASPLIT, heads, row segments). A segment is a run of at most 16 consecutive
-// rows of one sequence inside one 16-row tile: every token tile of a single sequence, or the
-// pieces of a batch of sequences cut at tile boundaries. Workgroup s takes chunks s,
-// s + ASPLIT, ... of its (head, segment) in order and keeps a running (max, sum, output) per
-// token (online softmax); the last of the ASPLIT workgroups to finish (an agent-scope counter)
-// merges their states in workgroup order and writes the output rows as fragments. Scores and the weighted
-// sum run on v_mfma_f32_16x16x4f32 (f32 products and sums): scores as [keys][tokens], one
-// 16-key block per wavefront; the output as [dims][tokens], one 16-dim block per wavefront.
-// Which chunks a workgroup takes depends only on key positions and ASPLIT, so a token's result
-// does not depend on how many tokens share the launch. The grid does not depend on the
-// position (read from the device), so the launch can be replayed from a graph.
+// One launch: grid (ASPLIT, heads, row segments) of 4-wavefront workgroups. A segment is a run
+// of at most 16 consecutive rows of one sequence inside one 16-row tile: every token tile of a
+// single sequence, or the pieces of a batch of sequences cut at tile boundaries. The keys are
+// cut into 16-key blocks; block b belongs to wavefront b % (4 ASPLIT) of the (head, segment)
+// (workgroup (b % (4 ASPLIT)) / 4), which keeps a running (max, sum, output) per token over its
+// blocks in order (online softmax) without any barrier: the scores ([keys][tokens]) and the
+// weighted sum ([dims][tokens]) run on v_mfma_f32_16x16x4f32 straight from registers, each lane
+// loading the K, V and q values it feeds (the next block's while this one computes). The four
+// wavefronts' states merge in LDS in wavefront order, and the last of the ASPLIT workgroups to
+// finish (an agent-scope counter) merges theirs in workgroup order and writes the output rows as
+// fragments. Which blocks a wavefront takes depends only on key positions, so a token's result
+// does not depend on how many tokens share the launch. The grid does not depend on the position
+// (read from the device), so the launch can be replayed from a graph.
 // ---------------------------------------------------------------------------------------
-constexpr int ACH = 64;    // keys per chunk
+constexpr int AKB = 16;    // keys per block
 constexpr int ATQ = 16;    // query tokens per tile
-constexpr int ASPLIT = 8;  // workgroups per (head, tile)
+constexpr int AWV = 4;     // wavefronts per workgroup
+constexpr int ASPLIT = 8;  // workgroups per (head, segment)
 constexpr int CPOL_SC1 = 16;
 constexpr int BUF_DWORD3 = 0x00020000;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -65,38 +68,75 @@ __device__ __forceinline__ f32x4 ld_f32x4(__amdgpu_buffer_rsrc_t r, int at) {
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
-// Row paddings keep the MFMA operand reads free of LDS bank conflicts: K and Q rows are read
-// as float4 by 16 lanes of consecutive rows (stride HD + 4), V rows by lane groups g on rows
-// 4 u + g (stride HD + 16).
+// MFMA operand layout (16x16x4 f32): lane l = 16 g + c supplies A[m = c][k = g] and B[k = g][n = c]
+// and receives D[m = 4 g + i][n = c], i < 4.
+//
+// Scores of block b, MFMA j < HD / 4: A = K[key 16 b + c][g HD/4 + j], B = q[token c][g HD/4 + j],
+// so lane (g, c) holds HD/4 consecutive floats of key row c and of query row c, and receives
+// the scores of keys 16 b + 4 g + i for token c. Weighted sum, output block db < DB = HD / 16,
+// MFMA u < 4: the keys of its K dimension are 16 b + 4 g + u, so B = p[16 b + 4 g + u][c] is the
+// lane's own score register u; its rows are dims DB m + db (m < 16), so A = V[16 b + 4 g + u]
+// [DB c + db] (lane (g, c) loads DB consecutive floats per key) and lane (g, c) receives dims
+// DB (4 g + i) + db of token c.
 template <int HD>
-struct AttnLds {
-    static constexpr int KP = HD + 4, VP = HD + 16, QP = HD + 4;
-    static constexpr int K = 0, V = K + ACH * KP, Q = V + ACH * VP, P = Q + ATQ * QP, R = P + ACH * ATQ, END = R + 2 * 4 * ATQ;
+struct AttnBlock {
+    static constexpr int H4 = HD / 4, DB = HD / 16;
+    float k[H4];
+    float v[4 * DB];
 };
 
-// Segment z: without a table, token tile z of one sequence whose row 0 sits at *pos0; with
-// one, segs[z] = (first row, rows, sequence, -) and each row's position is rows.pos[row].
+template <int HD>
+__device__ __forceinline__ void attn_load(AttnBlock<HD>& r, int b, int last_key, const float* __restrict__ kc,
+                                          const float* __restrict__ vc, int kv, int col0, int g, int c) {
+    constexpr int H4 = HD / 4, DB = HD / 16;
+    const int key = AKB * b + c;
+    if (key <= last_key) {
+        const float* kp = kc + size_t(key) * kv + col0 + g * H4;
+#pragma unroll
+        for (int j = 0; j < H4; j += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(kp + j);
+            r.k[j] = x.x;
+            r.k[j + 1] = x.y;
+            r.k[j + 2] = x.z;
+            r.k[j + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < H4; j++) r.k[j] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int vk = AKB * b + 4 * g + u;
+        const float* vp = vc + size_t(vk) * kv + col0 + DB * c;
+        if constexpr (DB % 4 == 0) {
+#pragma unroll
+            for (int db = 0; db < DB; db += 4) {
+                const float4 x = vk <= last_key ? *reinterpret_cast<const float4*>(vp + db) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                r.v[u * DB + db] = x.x;
+                r.v[u * DB + db + 1] = x.y;
+                r.v[u * DB + db + 2] = x.z;
+                r.v[u * DB + db + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int db = 0; db < DB; db++) r.v[u * DB + db] = vk <= last_key ? vp[db] : 0.0f;
+        }
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int ldq, int t, int heads, int kv_heads,
                                               const int* __restrict__ pos0p, AttnRows rows, float scale, const float* __restrict__ kc,
                                               const float* __restrict__ vc, float* pm, float* pl, float* po, int* cnt,
                                               uint8_t* __restrict__ frags, size_t frag_stride) {
-    using LY = AttnLds<HD>;
-    constexpr int KP = LY::KP, VP = LY::VP, QP = LY::QP, H4 = HD / 4;
-    constexpr int DB = HD / 16;                  // 16-dim blocks
-    constexpr int DBW = (DB + 3) / 4;            // dim blocks per wavefront
-    constexpr int NP = (ACH * H4 + 255) / 256;   // float4 pieces of K (and of V) per thread
-    extern __shared__ __align__(16) float sm[];
+    constexpr int H4 = HD / 4, DB = HD / 16;
+    __shared__ float sm_m[AWV][ATQ], sm_l[AWV][ATQ];
+    constexpr int HP = HD + 4;  // padded row of the wavefront outputs
+    __shared__ __align__(16) float sm_o[AWV * ATQ * HP];  // wavefront outputs [wave][token][dim], then the output rows
     __shared__ int flag;
-    float* Ks = sm + LY::K;
-    float* Vs = sm + LY::V;
-    float* Qs = sm + LY::Q;
-    float* Ps = sm + LY::P;   // [key][token]
-    float* Rm = sm + LY::R;   // [wave][token] chunk maxima
-    float* Rl = Rm + 4 * ATQ; // [wave][token] chunk sums
     const int s = blockIdx.x, head = blockIdx.y, seg = blockIdx.z;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, tok = lane & 15, g = lane >> 4;
-    const int kv = kv_heads * HD, grp = head / (heads / kv_heads);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+    const int kv = kv_heads * HD, col0 = (head / (heads / kv_heads)) * HD;
     int i0, nq, pos_first;  // first launch row, rows, position of the first row
     if (rows.segs) {
         const int4 sg = rows.segs[seg];
@@ -112,123 +152,120 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
     }
     const int tile = i0 / ATQ, tok0 = i0 % ATQ;  // fragment tile and token of the first row
     const int last_key = pos_first + nq - 1;
-    const int nc = last_key / ACH + 1;
+    const int nb = last_key / AKB + 1;
+    const int first = s * AWV + w, stride = ASPLIT * AWV;
     const size_t rows_total = size_t(t) * heads;
     const __amdgpu_buffer_rsrc_t rm = coherent_rsrc(pm, rows_total * ASPLIT * 4);
     const __amdgpu_buffer_rsrc_t rl = coherent_rsrc(pl, rows_total * ASPLIT * 4);
     const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(po, rows_total * ASPLIT * HD * 4);
 
-    auto load_kv = [&](int c, float4* kx, float4* vx) {
-        const int j0 = c * ACH, nk = min(ACH, last_key + 1 - j0);
+    AttnBlock<HD> ba, bb;
+    if (first < nb) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
+    float qr[H4];
+    {
+        const float* qp = q + size_t(i0 + c) * ldq + head * HD + g * H4;
 #pragma unroll
-        for (int u = 0; u < NP; u++) {
-            const int p = tid + u * 256, j = p / H4, d = 4 * (p % H4);
-            kx[u] = vx[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (p < ACH * H4 && j < nk) {
-                kx[u] = *reinterpret_cast<const float4*>(kc + size_t(j0 + j) * kv + grp * HD + d);
-                vx[u] = *reinterpret_cast<const float4*>(vc + size_t(j0 + j) * kv + grp * HD + d);
-            }
+        for (int j = 0; j < H4; j += 4) {
+            const float4 x = c < nq ? *reinterpret_cast<const float4*>(qp + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            qr[j] = x.x;
+            qr[j + 1] = x.y;
+            qr[j + 2] = x.z;
+            qr[j + 3] = x.w;
         }
-    };
-    float4 kx[NP], vx[NP];
-    if (s < nc) load_kv(s, kx, vx);
-    for (int p = tid; p < ATQ * H4; p += 256) {
-        const int i = p / H4, d = 4 * (p % H4);
-        *reinterpret_cast<float4*>(Qs + i * QP + d) =
-            i < nq ? *reinterpret_cast<const float4*>(q + size_t(i0 + i) * ldq + head * HD + d) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 
-    // Running state of token `tok` (every lane of that token holds the same M and L).
-    float M = -INFINITY, L = 0.0f;
-    f32x4 O[DBW];
+    // Running state of token c: M (the same in the four lanes of the token), this lane's share
+    // of the sum (keys 16 b + 4 g + i), and output dims 16 db + 4 g + i.
+    float M = -INFINITY, Lp = 0.0f;
+    f32x4 O[DB];
 #pragma unroll
-    for (int b = 0; b < DBW; b++) O[b] = f32x4{0, 0, 0, 0};
-
-    for (int c = s; c < nc; c += ASPLIT) {
-        const int j0 = c * ACH, nk = min(ACH, last_key + 1 - j0);
-        __syncthreads();  // the previous chunk is done with Ks, Vs, Ps
-#pragma unroll
-        for (int u = 0; u < NP; u++) {
-            const int p = tid + u * 256, j = p / H4, d = 4 * (p % H4);
-            if (p < ACH * H4) {
-                *reinterpret_cast<float4*>(Ks + j * KP + d) = kx[u];
-                *reinterpret_cast<float4*>(Vs + j * VP + d) = vx[u];
-            }
-        }
-        __syncthreads();
-        if (c + ASPLIT < nc) load_kv(c + ASPLIT, kx, vx);  // in flight during this chunk
-
-        // Scores [key 16 w + 4 g + i][token]: lane group g supplies dims g H4 + [0, H4).
+    for (int db = 0; db < DB; db++) O[db] = f32x4{0, 0, 0, 0};
+    auto block = [&](int b, const AttnBlock<HD>& r) {
         f32x4 sc = {0, 0, 0, 0};
 #pragma unroll
-        for (int d = 0; d < H4; d += 4) {
-            const float4 k4 = *reinterpret_cast<const float4*>(Ks + (16 * w + tok) * KP + g * H4 + d);
-            const float4 q4 = *reinterpret_cast<const float4*>(Qs + tok * QP + g * H4 + d);
-            sc = mfma_f32(k4.x, q4.x, sc);
-            sc = mfma_f32(k4.y, q4.y, sc);
-            sc = mfma_f32(k4.z, q4.z, sc);
-            sc = mfma_f32(k4.w, q4.w, sc);
-        }
-        // D of that product: lane (g, tok) holds keys 16 w + 4 g + i of token tok.
+        for (int j = 0; j < H4; j++) sc = mfma_f32(r.k[j], qr[j], sc);
         float sv[4];
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int j = 16 * w + 4 * g + i;
-            sv[i] = (tok < nq && j < nk && j0 + j <= pos_first + tok) ? sc[i] * scale : -INFINITY;
+            const int key = AKB * b + 4 * g + i;
+            sv[i] = (c < nq && key <= pos_first + c) ? sc[i] * scale : -INFINITY;
             mx = fmaxf(mx, sv[i]);
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        if (g == 0) Rm[w * ATQ + tok] = mx;
-        __syncthreads();
-        const float mc = fmaxf(fmaxf(Rm[tok], Rm[ATQ + tok]), fmaxf(Rm[2 * ATQ + tok], Rm[3 * ATQ + tok]));
-        const float Mn = fmaxf(M, mc);
+        const float Mn = fmaxf(M, mx);
         const float corr = M == -INFINITY ? 0.0f : expf(M - Mn);  // rescale of the running state
-        float ls = 0.0f;
+        float p[4], ls = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float e = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
-            Ps[(16 * w + 4 * g + i) * ATQ + tok] = e;
-            ls += e;
+            p[i] = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
+            ls += p[i];
         }
-        ls += __shfl_xor(ls, 16, 64);
-        ls += __shfl_xor(ls, 32, 64);
-        if (g == 0) Rl[w * ATQ + tok] = ls;
-        __syncthreads();
-        const float lc = ((Rl[tok] + Rl[ATQ + tok]) + Rl[2 * ATQ + tok]) + Rl[3 * ATQ + tok];
-        L = __builtin_fmaf(L, corr, lc);
+        Lp = __builtin_fmaf(Lp, corr, ls);
         M = Mn;
-        // Output [dim][token]: lane group g supplies keys 4 u + g.
 #pragma unroll
-        for (int b = 0; b < DBW; b++) {
-            const int db = w + 4 * b;
-            if (db < DB) {
-                f32x4 acc = {0, 0, 0, 0};
+        for (int db = 0; db < DB; db++) {
+            f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int u = 0; u < 16; u++) {
-                    const int key = 4 * u + g;
-                    acc = mfma_f32(Vs[key * VP + 16 * db + tok], Ps[key * ATQ + tok], acc);
-                }
+            for (int u = 0; u < 4; u++) acc = mfma_f32(r.v[u * DB + db], p[u], acc);
 #pragma unroll
-                for (int i = 0; i < 4; i++) O[b][i] = __builtin_fmaf(O[b][i], corr, acc[i]);
-            }
+            for (int i = 0; i < 4; i++) O[db][i] = __builtin_fmaf(O[db][i], corr, acc[i]);
+        }
+    };
+    for (int b = first; b < nb; b += 2 * stride) {
+        if (b + stride < nb) attn_load<HD>(bb, b + stride, last_key, kc, vc, kv, col0, g, c);
+        block(b, ba);
+        if (b + stride >= nb) break;
+        if (b + 2 * stride < nb) attn_load<HD>(ba, b + 2 * stride, last_key, kc, vc, kv, col0, g, c);
+        block(b + stride, bb);
+    }
+
+    // The four wavefronts' states, merged in wavefront order into this workgroup's state.
+    float L = Lp + __shfl_xor(Lp, 16, 64);
+    L += __shfl_xor(L, 32, 64);
+    if (g == 0) {
+        sm_m[w][c] = M;
+        sm_l[w][c] = L;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float* dst = &sm_o[(w * ATQ + c) * HP + DB * (4 * g + i)];  // dims DB (4 g + i) + [0, DB)
+        if constexpr (DB % 4 == 0) {
+#pragma unroll
+            for (int db = 0; db < DB; db += 4)
+                *reinterpret_cast<f32x4*>(dst + db) = f32x4{O[db][i], O[db + 1][i], O[db + 2][i], O[db + 3][i]};
+        } else {
+#pragma unroll
+            for (int db = 0; db < DB; db++) dst[db] = O[db][i];
         }
     }
-    // This workgroup's state: lane (g, tok) of wavefront w holds dims 16 (w + 4 b) + 4 g + [0, 4).
-    // O is [dims][tokens] per lane: transpose the lane view. D of the output product: lane l
-    // holds dims 16 db + 4 (l / 16) + i of token l % 16.
-    if (tok < nq) {
-        const size_t row = (size_t(i0 + tok) * heads + head) * ASPLIT + s;
-        if (w == 0 && g == 0) {
-            st_f32(M, rm, int(row * 4));
-            st_f32(L, rl, int(row * 4));
-        }
+    __syncthreads();
+    for (int e = tid; e < ATQ * (HD / 4); e += AWV * 64) {
+        const int tk = e % ATQ, d = 4 * (e / ATQ);
+        if (tk >= nq) continue;
+        float mw[AWV], Mx = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < DBW; b++) {
-            const int db = w + 4 * b;
-            if (db < DB) st_f32x4(O[b], ro, int((row * HD + 16 * db + 4 * g) * 4));
+        for (int k = 0; k < AWV; k++) {
+            mw[k] = sm_m[k][tk];
+            Mx = fmaxf(Mx, mw[k]);
         }
+        float Lw = 0.0f;
+        f32x4 ow = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < AWV; k++) {
+            const float e2 = mw[k] == -INFINITY ? 0.0f : expf(mw[k] - Mx);
+            Lw = __builtin_fmaf(sm_l[k][tk], e2, Lw);
+            const f32x4 x = *reinterpret_cast<const f32x4*>(&sm_o[(k * ATQ + tk) * HP + d]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) ow[i] = __builtin_fmaf(x[i], e2, ow[i]);
+        }
+        const size_t row = (size_t(i0 + tk) * heads + head) * ASPLIT + s;
+        if (d == 0) {
+            st_f32(Mx, rm, int(row * 4));
+            st_f32(Lw, rl, int(row * 4));
+        }
+        st_f32x4(ow, ro, int((row * HD + d) * 4));
     }
 
     // The last workgroup of (head, segment) merges the ASPLIT states in order.
@@ -244,7 +281,7 @@ __global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int l
     __syncthreads();
     if (!flag) return;
     constexpr int DPT = HD / 16;  // dims per thread: thread (row, sub) takes sub * DPT ..
-    float* Os = sm;               // [ATQ][HD] output rows
+    float* Os = sm_o;             // [ATQ][HD] output rows
     const int row = tid >> 4, sub = tid & 15;
     if (row < nq) {
         const size_t base = (size_t(i0 + row) * heads + head) * ASPLIT;
@@ -300,11 +337,9 @@ static void launch_attn(const float* q, int ldq, int t, int heads, int kv_heads,
     float* pm = scratch;
     float* pl = pm + size_t(t) * heads * ASPLIT;
     float* po = pl + size_t(t) * heads * ASPLIT;
-    using LY = AttnLds<HD>;
-    const size_t lds = sizeof(float) * size_t(LY::END);
     const float scale = 1.0f / sqrtf(float(HD));
     const int nseg = rows.segs ? rows.n_segs : (t + ATQ - 1) / ATQ;
-    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(256), lds, s, q, ldq, t, heads, kv_heads, pos0, rows,
+    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(AWV * 64), 0, s, q, ldq, t, heads, kv_heads, pos0, rows,
                        scale, kc, vc, pm, pl, po, cnt, frags, frag_tile_bytes(heads * HD));
     HIPCHECK(hipGetLastError());
 }
