@@ -6,7 +6,14 @@
 #include <cstddef>
 #include <cstdint>
 
+#include "fused.hpp"
+
 namespace ls {
+
+// Cache policy of data handed between workgroups of one launch: sc1, coherent across the L2s
+// of the XCDs.
+constexpr int CPOL_SC1 = 16;
+constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
 
 // f32 value -> three bf16 terms (truncations) whose sum is the value exactly.
 __device__ __forceinline__ void split3(float v, uint32_t& h, uint32_t& m, uint32_t& l) {
@@ -58,6 +65,46 @@ __device__ __forceinline__ void write_slot_coherent(__amdgpu_buffer_rsrc_t r, si
     __builtin_amdgcn_raw_buffer_store_b128(u32x4_{H[0], H[1], H[2], H[3]}, r, at, 0, 16);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4_{M[0], M[1], M[2], M[3]}, r, at + 64 * 16, 0, 16);
     __builtin_amdgcn_raw_buffer_store_b128(u32x4_{L[0], L[1], L[2], L[3]}, r, at + 128 * 16, 0, 16);
+}
+
+// Waits of the in-launch dataflow (see Flow). Thread 0 polls with atomic adds of zero: a plain
+// load, even at agent scope, can keep hitting this XCD's L2 copy of the line for microseconds,
+// while an atomic is served at the coherence point. The zero is hidden from the compiler, which
+// would otherwise turn the idempotent atomic back into a load. After a bounded number of sleeps
+// the wait records an error and goes on, so every wave ends.
+constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
+
+__device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
+    if (threadIdx.x == 0) {
+        int* cnt = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + j);
+        const int want = min(fl.producers, fl.per * (j + 1)) - fl.per * j;
+        int zero = 0;
+        asm volatile("" : "+v"(zero));
+        unsigned spins = 0;
+        while (__hip_atomic_fetch_add(cnt, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+            if (++spins > FLOW_SPIN_LIMIT) {
+                __hip_atomic_store(fl.ctl + FLOW_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        const int old = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == fl.consumers - 1) {
+            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+}
+
+// Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
+// moves.
+__device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + r / fl.per), 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace ls

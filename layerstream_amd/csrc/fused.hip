@@ -11,6 +11,7 @@
 // arithmetic depends only on the matrix shape, never on the number of tokens in the launch: a
 // verify pass over k+1 tokens gives the same bits as k+1 single-token passes (src/spec.rs:8-11).
 #include "fused.hpp"
+#include "attn_dev.hpp"
 #include "frag_dev.hpp"
 
 #include <hip/hip_ext.h>
@@ -424,51 +425,8 @@ __device__ __forceinline__ int qkv_ref_row(int row, int hd, int qk_rows) {
     return row - r + ((r & 1) ? hd / 2 + (r >> 1) : (r >> 1));
 }
 
-// Cache policy of the split-K pieces: sc1, coherent across the L2s of the XCDs.
-constexpr int CPOL_SC1 = 16;
-constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
 constexpr int MAX_SPLIT = 16;
 constexpr int ROPE_HALF_MAX = 128;
-
-// Waits of the in-launch dataflow (see Flow). Thread 0 polls with atomic adds of zero: a plain
-// load, even at agent scope, can keep hitting this XCD's L2 copy of the line for microseconds,
-// while an atomic is served at the coherence point. The zero is hidden from the compiler, which
-// would otherwise turn the idempotent atomic back into a load. After a bounded number of sleeps
-// the wait records an error and goes on, so every wave ends.
-constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
-
-__device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
-    if (threadIdx.x == 0) {
-        int* cnt = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * j;
-        const int want = min(fl.producers, fl.per * (j + 1)) - fl.per * j;
-        int zero = 0;
-        asm volatile("" : "+v"(zero));
-        unsigned spins = 0;
-        while (__hip_atomic_fetch_add(cnt, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
-            if (++spins > FLOW_SPIN_LIMIT) {
-                __hip_atomic_store(fl.ctl + FLOW_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        const int old = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == fl.consumers - 1) {
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-    __syncthreads();
-}
-
-// Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
-// moves.
-__device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (r / fl.per), 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
 // [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
@@ -812,6 +770,24 @@ __global__ __launch_bounds__(1024) void k_gu_down(MMArgs gu, MMPlan pgu, MMArgs 
     }
 }
 
+// Attention and the o projection in one launch (one token tile): workgroups [0, ASPLIT heads)
+// run attention, and the one that merges a head's states writes its output fragments through
+// the coherent path and counts the head done; the o workgroups after them load their weights,
+// wait for every head, then read the fragments coherently. Every attention workgroup has a lower
+// index than every o workgroup, so it is dispatched first, and it never waits.
+template <int HD, int BITS, bool G16>
+__global__ __launch_bounds__(512) void k_attn_o(AttnArgs aa, MMArgs o, MMPlan po, MMScratch sc, Flow fl) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int na = ASPLIT * aa.heads;
+    if (int(blockIdx.x) < na) {
+        if (int(threadIdx.x) >= AWV * 64) return;
+        attn_body<HD, true>(aa, int(blockIdx.x) % ASPLIT, int(blockIdx.x) / ASPLIT, 0, fl);
+    } else {
+        if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
+        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fl, int(blockIdx.x) - na, 0, smem);
+    }
+}
+
 // Output head, persistent: each workgroup copies the tile's fragments (every k-step) to LDS
 // once; its wavefronts then stream 64-row groups of the table over the whole K range, PF chunks
 // ahead, and reduce each group to logits and a per-token (value, index) argmax partial inside
@@ -1090,6 +1066,49 @@ void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, cons
             break;
     }
     FCHECK(hipGetLastError());
+}
+
+int attention_o_workgroups(int heads, const MMPlan& po) { return ASPLIT * heads + po.nrb * po.nsplit; }
+
+template <int HD>
+static void launch_attn_o(const AttnArgs& aa, const MMArgs& o, const MMPlan& po, const MMScratch& sc, const Flow& fl, hipStream_t s) {
+    const dim3 grid(attention_o_workgroups(aa.heads, po)), block(std::max(AWV * 64, 64 * po.rg * po.kw));
+    const size_t lds = lds_bytes(po);
+    const bool g16 = o.W.bits != 16 && o.W.group == 16;
+    switch (o.W.bits) {
+        case 16: go(k_attn_o<HD, 16, false>, grid, block, lds, s, aa, o, po, sc, fl); break;
+        case 8:
+            if (g16) go(k_attn_o<HD, 8, true>, grid, block, lds, s, aa, o, po, sc, fl);
+            else go(k_attn_o<HD, 8, false>, grid, block, lds, s, aa, o, po, sc, fl);
+            break;
+        default:
+            if (g16) go(k_attn_o<HD, 4, true>, grid, block, lds, s, aa, o, po, sc, fl);
+            else go(k_attn_o<HD, 4, false>, grid, block, lds, s, aa, o, po, sc, fl);
+            break;
+    }
+    FCHECK(hipGetLastError());
+}
+
+void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd, const int* pos0, const float* kc, const float* vc,
+                 float* scratch, int* cnt, uint8_t* frags, const MMArgs& o, const MMPlan& po, const MMScratch& sc, int* ctl,
+                 hipStream_t s) {
+    if (t > FTOK || po.tiles != 1) throw std::runtime_error("the fused attention/o launch takes one token tile");
+    if (po.s != 1 || po.nsplit != 1) throw std::runtime_error("the fused attention/o launch needs o without a K split");
+    if (64 * po.rg * po.kw > 512) throw std::runtime_error("o workgroups too large for the fused attention/o launch");
+    const AttnArgs aa = make_attn_args(q, ldq, t, heads, kv_heads, hd, pos0, AttnRows{}, kc, vc, scratch, cnt, frags);
+    Flow fl;
+    fl.ctl = ctl;
+    fl.producers = heads;
+    fl.per = heads;
+    fl.consumers = po.nrb * po.nsplit;
+    fl.base = FLOW_ATTN_O;
+    switch (hd) {
+        case 16: launch_attn_o<16>(aa, o, po, sc, fl, s); break;
+        case 32: launch_attn_o<32>(aa, o, po, sc, fl, s); break;
+        case 64: launch_attn_o<64>(aa, o, po, sc, fl, s); break;
+        case 128: launch_attn_o<128>(aa, o, po, sc, fl, s); break;
+        default: throw std::runtime_error("head_dim must be 16, 32, 64 or 128");
+    }
 }
 
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {

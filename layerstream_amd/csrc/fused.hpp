@@ -149,9 +149,11 @@ struct Flow {
     int producers = 0;
     int per = 1;        // producers per counter
     int consumers = 0;  // consumer workgroups per counter
+    int base = 0;       // first counter of this launch
 };
-// Control block words: error flag, greedy acceptance (m, next), then the counters.
-enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 16 };
+// Control block words: error flag, greedy acceptance (m, next), then the counters (gate|up ->
+// down from counter 0, attention -> o at FLOW_ATTN_O).
+enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 16, FLOW_ATTN_O = FLOW_COUNTERS - 1 };
 constexpr int FLOW_WORDS = FLOW_CNT0 + FLOW_CNT_STRIDE * FLOW_COUNTERS;
 
 // QKV projection + 1/rms + bias + RoPE + K/V append (plan strips 1). Rows: q heads and k heads
@@ -169,6 +171,15 @@ void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream
 // block (FLOW_WORDS ints).
 void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, const MMPlan& pdn, const MMScratch& sc,
                      int* ctl, hipStream_t s);
+// Attention (one token tile of one sequence, see attention() in kernels.hpp) and the o
+// projection (mm_residual, plan strips 1 without a K split) in one launch: the o workgroups
+// load their weights while attention runs. ctl is the control block.
+void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd, const int* pos0, const float* kc, const float* vc,
+                 float* scratch, int* cnt, uint8_t* frags, const MMArgs& o, const MMPlan& po, const MMScratch& sc, int* ctl,
+                 hipStream_t s);
+// Workgroups of an attention_o launch (its grid, one workgroup per CU at most).
+int attention_o_workgroups(int heads, const MMPlan& po);
+
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
 // partials at [tile][arg_off + b][16] for b below the returned count.
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);

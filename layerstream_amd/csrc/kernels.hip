@@ -10,6 +10,7 @@
 
 #include "kernels.hpp"
 
+#include "attn_dev.hpp"
 #include "frag_dev.hpp"
 #include "fused.hpp"
 
@@ -21,312 +22,9 @@ namespace ls {
         if (e_ != hipSuccess) throw std::runtime_error(std::string("HIP: ") + hipGetErrorString(e_)); \
     } while (0)
 
-// ---------------------------------------------------------------------------------------
-// Causal GQA attention (src/model.rs:261-282), flash-decoding. The reference computes scores
-// (q . k_j) * scale, a softmax (max, exp(x - max), sum, * 1/sum) and sum_j p_j v_j over every
-// cached position.
-//
-// One launch: grid (ASPLIT, heads, row segments) of 4-wavefront workgroups. A segment is a run
-// of at most 16 consecutive rows of one sequence inside one 16-row tile: every token tile of a
-// single sequence, or the pieces of a batch of sequences cut at tile boundaries. The keys are
-// cut into 16-key blocks; block b belongs to wavefront b % (4 ASPLIT) of the (head, segment)
-// (workgroup (b % (4 ASPLIT)) / 4), which keeps a running (max, sum, output) per token over its
-// blocks in order (online softmax) without any barrier: the scores ([keys][tokens]) and the
-// weighted sum ([dims][tokens]) run on v_mfma_f32_16x16x4f32 straight from registers, each lane
-// loading the K, V and q values it feeds (the next block's while this one computes). The four
-// wavefronts' states merge in LDS in wavefront order, and the last of the ASPLIT workgroups to
-// finish (an agent-scope counter) merges theirs in workgroup order and writes the output rows as
-// fragments. Which blocks a wavefront takes depends only on key positions, so a token's result
-// does not depend on how many tokens share the launch. The grid does not depend on the position
-// (read from the device), so the launch can be replayed from a graph.
-// ---------------------------------------------------------------------------------------
-constexpr int AKB = 16;    // keys per block
-constexpr int ATQ = 16;    // query tokens per tile
-constexpr int AWV = 4;     // wavefronts per workgroup
-constexpr int ASPLIT = 8;  // workgroups per (head, segment)
-constexpr int CPOL_SC1 = 16;
-constexpr int BUF_DWORD3 = 0x00020000;
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* p, size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), BUF_DWORD3);
-}
-// Coherent (sc1) float accesses; the buffer builtins move raw 32-bit words.
-__device__ __forceinline__ void st_f32(float v, __amdgpu_buffer_rsrc_t r, int at) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, at, 0, CPOL_SC1);
-}
-__device__ __forceinline__ float ld_f32(__amdgpu_buffer_rsrc_t r, int at) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, at, 0, CPOL_SC1));
-}
-__device__ __forceinline__ void st_f32x4(f32x4 v, __amdgpu_buffer_rsrc_t r, int at) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, at, 0, CPOL_SC1);
-}
-__device__ __forceinline__ f32x4 ld_f32x4(__amdgpu_buffer_rsrc_t r, int at) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, at, 0, CPOL_SC1));
-}
-
-__device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
-
-// MFMA operand layout (16x16x4 f32): lane l = 16 g + c supplies A[m = c][k = g] and B[k = g][n = c]
-// and receives D[m = 4 g + i][n = c], i < 4.
-//
-// Scores of block b, MFMA j < HD / 4: A = K[key 16 b + c][g HD/4 + j], B = q[token c][g HD/4 + j],
-// so lane (g, c) holds HD/4 consecutive floats of key row c and of query row c, and receives
-// the scores of keys 16 b + 4 g + i for token c. Weighted sum, output block db < DB = HD / 16,
-// MFMA u < 4: the keys of its K dimension are 16 b + 4 g + u, so B = p[16 b + 4 g + u][c] is the
-// lane's own score register u; its rows are dims DB m + db (m < 16), so A = V[16 b + 4 g + u]
-// [DB c + db] (lane (g, c) loads DB consecutive floats per key) and lane (g, c) receives dims
-// DB (4 g + i) + db of token c.
 template <int HD>
-struct AttnBlock {
-    static constexpr int H4 = HD / 4, DB = HD / 16;
-    float k[H4];
-    float v[4 * DB];
-};
-
-template <int HD>
-__device__ __forceinline__ void attn_load(AttnBlock<HD>& r, int b, int last_key, const float* __restrict__ kc,
-                                          const float* __restrict__ vc, int kv, int col0, int g, int c) {
-    constexpr int H4 = HD / 4, DB = HD / 16;
-    const int key = AKB * b + c;
-    if (key <= last_key) {
-        const float* kp = kc + size_t(key) * kv + col0 + g * H4;
-#pragma unroll
-        for (int j = 0; j < H4; j += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(kp + j);
-            r.k[j] = x.x;
-            r.k[j + 1] = x.y;
-            r.k[j + 2] = x.z;
-            r.k[j + 3] = x.w;
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < H4; j++) r.k[j] = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int vk = AKB * b + 4 * g + u;
-        const float* vp = vc + size_t(vk) * kv + col0 + DB * c;
-        if constexpr (DB % 4 == 0) {
-#pragma unroll
-            for (int db = 0; db < DB; db += 4) {
-                const float4 x = vk <= last_key ? *reinterpret_cast<const float4*>(vp + db) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                r.v[u * DB + db] = x.x;
-                r.v[u * DB + db + 1] = x.y;
-                r.v[u * DB + db + 2] = x.z;
-                r.v[u * DB + db + 3] = x.w;
-            }
-        } else {
-#pragma unroll
-            for (int db = 0; db < DB; db++) r.v[u * DB + db] = vk <= last_key ? vp[db] : 0.0f;
-        }
-    }
-}
-
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn(const float* __restrict__ q, int ldq, int t, int heads, int kv_heads,
-                                              const int* __restrict__ pos0p, AttnRows rows, float scale, const float* __restrict__ kc,
-                                              const float* __restrict__ vc, float* pm, float* pl, float* po, int* cnt,
-                                              uint8_t* __restrict__ frags, size_t frag_stride) {
-    constexpr int H4 = HD / 4, DB = HD / 16;
-    __shared__ float sm_m[AWV][ATQ], sm_l[AWV][ATQ];
-    constexpr int HP = HD + 4;  // padded row of the wavefront outputs
-    __shared__ __align__(16) float sm_o[AWV * ATQ * HP];  // wavefront outputs [wave][token][dim], then the output rows
-    __shared__ int flag;
-    const int s = blockIdx.x, head = blockIdx.y, seg = blockIdx.z;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
-    const int kv = kv_heads * HD, col0 = (head / (heads / kv_heads)) * HD;
-    int i0, nq, pos_first;  // first launch row, rows, position of the first row
-    if (rows.segs) {
-        const int4 sg = rows.segs[seg];
-        i0 = sg.x;
-        nq = sg.y;
-        pos_first = rows.pos[i0];
-        kc += size_t(sg.z) * rows.seq_stride;
-        vc += size_t(sg.z) * rows.seq_stride;
-    } else {
-        i0 = seg * ATQ;
-        nq = min(ATQ, t - i0);
-        pos_first = *pos0p + i0;
-    }
-    const int tile = i0 / ATQ, tok0 = i0 % ATQ;  // fragment tile and token of the first row
-    const int last_key = pos_first + nq - 1;
-    const int nb = last_key / AKB + 1;
-    const int first = s * AWV + w, stride = ASPLIT * AWV;
-    const size_t rows_total = size_t(t) * heads;
-    const __amdgpu_buffer_rsrc_t rm = coherent_rsrc(pm, rows_total * ASPLIT * 4);
-    const __amdgpu_buffer_rsrc_t rl = coherent_rsrc(pl, rows_total * ASPLIT * 4);
-    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(po, rows_total * ASPLIT * HD * 4);
-
-    AttnBlock<HD> ba, bb;
-    if (first < nb) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
-    float qr[H4];
-    {
-        const float* qp = q + size_t(i0 + c) * ldq + head * HD + g * H4;
-#pragma unroll
-        for (int j = 0; j < H4; j += 4) {
-            const float4 x = c < nq ? *reinterpret_cast<const float4*>(qp + j) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            qr[j] = x.x;
-            qr[j + 1] = x.y;
-            qr[j + 2] = x.z;
-            qr[j + 3] = x.w;
-        }
-    }
-
-    // Running state of token c: M (the same in the four lanes of the token), this lane's share
-    // of the sum (keys 16 b + 4 g + i), and output dims 16 db + 4 g + i.
-    float M = -INFINITY, Lp = 0.0f;
-    f32x4 O[DB];
-#pragma unroll
-    for (int db = 0; db < DB; db++) O[db] = f32x4{0, 0, 0, 0};
-    auto block = [&](int b, const AttnBlock<HD>& r) {
-        f32x4 sc = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < H4; j++) sc = mfma_f32(r.k[j], qr[j], sc);
-        float sv[4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int key = AKB * b + 4 * g + i;
-            sv[i] = (c < nq && key <= pos_first + c) ? sc[i] * scale : -INFINITY;
-            mx = fmaxf(mx, sv[i]);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float Mn = fmaxf(M, mx);
-        const float corr = M == -INFINITY ? 0.0f : expf(M - Mn);  // rescale of the running state
-        float p[4], ls = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            p[i] = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
-            ls += p[i];
-        }
-        Lp = __builtin_fmaf(Lp, corr, ls);
-        M = Mn;
-#pragma unroll
-        for (int db = 0; db < DB; db++) {
-            f32x4 acc = {0, 0, 0, 0};
-#pragma unroll
-            for (int u = 0; u < 4; u++) acc = mfma_f32(r.v[u * DB + db], p[u], acc);
-#pragma unroll
-            for (int i = 0; i < 4; i++) O[db][i] = __builtin_fmaf(O[db][i], corr, acc[i]);
-        }
-    };
-    for (int b = first; b < nb; b += 2 * stride) {
-        if (b + stride < nb) attn_load<HD>(bb, b + stride, last_key, kc, vc, kv, col0, g, c);
-        block(b, ba);
-        if (b + stride >= nb) break;
-        if (b + 2 * stride < nb) attn_load<HD>(ba, b + 2 * stride, last_key, kc, vc, kv, col0, g, c);
-        block(b + stride, bb);
-    }
-
-    // The four wavefronts' states, merged in wavefront order into this workgroup's state.
-    float L = Lp + __shfl_xor(Lp, 16, 64);
-    L += __shfl_xor(L, 32, 64);
-    if (g == 0) {
-        sm_m[w][c] = M;
-        sm_l[w][c] = L;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        float* dst = &sm_o[(w * ATQ + c) * HP + DB * (4 * g + i)];  // dims DB (4 g + i) + [0, DB)
-        if constexpr (DB % 4 == 0) {
-#pragma unroll
-            for (int db = 0; db < DB; db += 4)
-                *reinterpret_cast<f32x4*>(dst + db) = f32x4{O[db][i], O[db + 1][i], O[db + 2][i], O[db + 3][i]};
-        } else {
-#pragma unroll
-            for (int db = 0; db < DB; db++) dst[db] = O[db][i];
-        }
-    }
-    __syncthreads();
-    for (int e = tid; e < ATQ * (HD / 4); e += AWV * 64) {
-        const int tk = e % ATQ, d = 4 * (e / ATQ);
-        if (tk >= nq) continue;
-        float mw[AWV], Mx = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < AWV; k++) {
-            mw[k] = sm_m[k][tk];
-            Mx = fmaxf(Mx, mw[k]);
-        }
-        float Lw = 0.0f;
-        f32x4 ow = {0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < AWV; k++) {
-            const float e2 = mw[k] == -INFINITY ? 0.0f : expf(mw[k] - Mx);
-            Lw = __builtin_fmaf(sm_l[k][tk], e2, Lw);
-            const f32x4 x = *reinterpret_cast<const f32x4*>(&sm_o[(k * ATQ + tk) * HP + d]);
-#pragma unroll
-            for (int i = 0; i < 4; i++) ow[i] = __builtin_fmaf(x[i], e2, ow[i]);
-        }
-        const size_t row = (size_t(i0 + tk) * heads + head) * ASPLIT + s;
-        if (d == 0) {
-            st_f32(Mx, rm, int(row * 4));
-            st_f32(Lw, rl, int(row * 4));
-        }
-        st_f32x4(ow, ro, int((row * HD + d) * 4));
-    }
-
-    // The last workgroup of (head, segment) merges the ASPLIT states in order.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        int* cn = cnt + size_t(seg) * heads + head;
-        const int old = __hip_atomic_fetch_add(cn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == ASPLIT - 1;
-        if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        flag = last;
-    }
-    __syncthreads();
-    if (!flag) return;
-    constexpr int DPT = HD / 16;  // dims per thread: thread (row, sub) takes sub * DPT ..
-    float* Os = sm_o;             // [ATQ][HD] output rows
-    const int row = tid >> 4, sub = tid & 15;
-    if (row < nq) {
-        const size_t base = (size_t(i0 + row) * heads + head) * ASPLIT;
-        float mv[ASPLIT], lv[ASPLIT], ov[ASPLIT][DPT];
-#pragma unroll
-        for (int k = 0; k < ASPLIT; k++) {
-            mv[k] = ld_f32(rm, int((base + k) * 4));
-            lv[k] = ld_f32(rl, int((base + k) * 4));
-            if constexpr (DPT % 4 == 0) {
-#pragma unroll
-                for (int u = 0; u < DPT; u += 4) {
-                    const f32x4 x = ld_f32x4(ro, int(((base + k) * HD + sub * DPT + u) * 4));
-                    ov[k][u] = x[0];
-                    ov[k][u + 1] = x[1];
-                    ov[k][u + 2] = x[2];
-                    ov[k][u + 3] = x[3];
-                }
-            } else {
-#pragma unroll
-                for (int u = 0; u < DPT; u++) ov[k][u] = ld_f32(ro, int(((base + k) * HD + sub * DPT + u) * 4));
-            }
-        }
-        float Mx = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < ASPLIT; k++) Mx = fmaxf(Mx, mv[k]);
-        float Lt = 0.0f, o[DPT];
-#pragma unroll
-        for (int u = 0; u < DPT; u++) o[u] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < ASPLIT; k++) {
-            const float e = mv[k] == -INFINITY ? 0.0f : expf(mv[k] - Mx);
-            Lt = __builtin_fmaf(lv[k], e, Lt);
-#pragma unroll
-            for (int u = 0; u < DPT; u++) o[u] = __builtin_fmaf(ov[k][u], e, o[u]);
-        }
-        const float inv = 1.0f / Lt;
-#pragma unroll
-        for (int u = 0; u < DPT; u++) Os[row * HD + sub * DPT + u] = o[u] * inv;
-    }
-    __syncthreads();
-    uint8_t* tf = frags + size_t(tile) * frag_stride;
-    for (int p = tid; p < nq * (HD / 8); p += 256) {
-        const int i = p / (HD / 8), sl = p % (HD / 8), col = head * HD + 8 * sl;
-        write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
-    }
+__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+    attn_body<HD, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, Flow{});
 }
 
 size_t attention_scratch_floats(int t, int heads, int hd, int) { return size_t(t) * heads * ASPLIT * (hd + 2); }
@@ -334,13 +32,9 @@ size_t attention_scratch_floats(int t, int heads, int hd, int) { return size_t(t
 template <int HD>
 static void launch_attn(const float* q, int ldq, int t, int heads, int kv_heads, const int* pos0, const AttnRows& rows,
                         const float* kc, const float* vc, float* scratch, int* cnt, uint8_t* frags, hipStream_t s) {
-    float* pm = scratch;
-    float* pl = pm + size_t(t) * heads * ASPLIT;
-    float* po = pl + size_t(t) * heads * ASPLIT;
-    const float scale = 1.0f / sqrtf(float(HD));
+    const AttnArgs a = make_attn_args(q, ldq, t, heads, kv_heads, HD, pos0, rows, kc, vc, scratch, cnt, frags);
     const int nseg = rows.segs ? rows.n_segs : (t + ATQ - 1) / ATQ;
-    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(AWV * 64), 0, s, q, ldq, t, heads, kv_heads, pos0, rows,
-                       scale, kc, vc, pm, pl, po, cnt, frags, frag_tile_bytes(heads * HD));
+    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(AWV * 64), 0, s, a);
     HIPCHECK(hipGetLastError());
 }
 

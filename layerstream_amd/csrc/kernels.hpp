@@ -26,6 +26,7 @@ struct AttnRows {
 // (fused.hpp) into `frags`, tile stride frag_tile_bytes(heads * hd). scratch holds
 // attention_scratch_floats() floats; cnt holds one counter per (segment, head) (ceil(t / 16)
 // segments without a table), zero at the start and left at zero.
+constexpr int ATTN_SPLIT = 8;  // workgroups per (head, segment)
 size_t attention_scratch_floats(int t, int heads, int hd, int max_ctx);
 void attention(const float* q, int ldq, int t, int heads, int kv_heads, int hd, const int* pos0, const AttnRows& rows,
                const float* k_cache, const float* v_cache, float* scratch, int* cnt, uint8_t* frags, hipStream_t s);

@@ -586,14 +586,14 @@ void Model::prof_begin() {
     mm_time_next_launch(prof_ev_[prof_used_], prof_ev_[prof_used_ + 1]);
 }
 
-void Model::prof_end(const TMat& W, int nt, bool launch) {
+void Model::prof_end(const TMat& W, int nt, bool launch, double extra_bytes) {
     if (!prof_) return;
     const Format f{W.bits, W.group};
     if (launch) {
         prof_used_ += 2;
         prof_acc_.launches++;
     }
-    prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * nt * (double(W.cols) + double(W.rows));
+    prof_acc_.bytes += double(W.rows) * double(f.row_bytes(size_t(W.cols))) + 4.0 * nt * (double(W.cols) + double(W.rows)) + extra_bytes;
     prof_acc_.flops += 2.0 * nt * double(W.rows) * double(W.cols);
 }
 
@@ -712,8 +712,6 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             mm_qkv(a, mm_plan(L.qkv, 1, kw_qkv_, T, 1), scr, s);
             prof_end(L.qkv, T);
         }
-        attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, bv ? bv->attn : AttnRows{}, kc, vc, attn_scratch_.as<float>(),
-                  attn_cnt_.as<int>(), af_.as<uint8_t>(), s);
         {
             MMArgs a;
             a.W = L.o;
@@ -727,9 +725,22 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.onorm = L.post_norm;
             a.oss = ss;
             a.oss_slots = slots_h_;
-            prof_begin();
-            mm_residual(a, mm_plan(L.o, 1, kw_o_, T, 1), scr, s);
-            prof_end(L.o, T);
+            const MMPlan po = mm_plan(L.o, 1, kw_o_, T, 1);
+            // One launch for attention and o when the o workgroups can fetch their weights while
+            // attention runs (one token tile, every workgroup resident at once).
+            if (fuse_on_ && !bv && po.tiles == 1 && po.nsplit == 1 && 64 * po.rg * po.kw <= 512 &&
+                attention_o_workgroups(heads, po) <= device_cu_count()) {
+                prof_begin();
+                attention_o(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, kc, vc, attn_scratch_.as<float>(), attn_cnt_.as<int>(),
+                            af_.as<uint8_t>(), a, po, scr, ctl_.as<int>(), s);
+                prof_end(L.o, T, true, 2.0 * kv * 4 * double(pos_ + T));  // + the K/V rows attention reads
+            } else {
+                attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, bv ? bv->attn : AttnRows{}, kc, vc, attn_scratch_.as<float>(),
+                          attn_cnt_.as<int>(), af_.as<uint8_t>(), s);
+                prof_begin();
+                mm_residual(a, po, scr, s);
+                prof_end(L.o, T);
+            }
         }
         {
             MMArgs g;

@@ -152,7 +152,7 @@ private:
     void plan_kw_from_env();
     void harvest();
     void prof_begin();
-    void prof_end(const TMat& W, int nt, bool launch = true);
+    void prof_end(const TMat& W, int nt, bool launch = true, double extra_bytes = 0);
     void check_flow(const int* ctl);
 
     Config cfg_;
