@@ -37,8 +37,12 @@ def gpu_model(m, mode=LS.MODE_RESIDENT, slots=2, max_ctx=128):
     return LS.Model(src, mode, slots, max_ctx)
 
 
+# The oracle's threads: the cores this process may run on, at most 16 (a GPU's share of its host).
+ORACLE_THREADS = max(1, min(16, len(os.sched_getaffinity(0))))
+
+
 def cpu_model(m, max_ctx=128):
-    return O.OracleModel(oracle_cfg(m["config_text"]), m["layers"], m["embed"], m["norm"], threads=os.cpu_count() or 4, max_ctx=max_ctx)
+    return O.OracleModel(oracle_cfg(m["config_text"]), m["layers"], m["embed"], m["norm"], threads=ORACLE_THREADS, max_ctx=max_ctx)
 
 
 def bits(a):
@@ -396,3 +400,62 @@ def test_qwen05b_int8_greedy_after_a_512_token_prompt_matches_the_oracle():
     d = LS.ScriptedDrafter(g, 0.6, 7, 151936)
     got, st = LS.speculative_greedy(gpu_model(m, max_ctx=1024), d, prompt, n, 8)
     assert got == g and st["target_passes"] < n
+
+
+def qwen3b(fmt, seed=1):
+    text = LS.qwen2_config_text(**LS.QWEN2_3B)
+    m = LS.synth_bf16_model(text, seed)
+    img = LS.quantize_model(text, m["layers"], m["embed"], m["norm"], fmt)
+    del m
+    parts = T.split_lsq(img.tobytes(), oracle_cfg(LS.inject_quant(text, *fmt)))
+    return {"config_text": LS.inject_quant(text, *fmt), "lsq": img, **{k: parts[k] for k in ("layers", "embed", "norm")}}
+
+
+def verify_step_vs_oracle(m, prompt, k, rng, max_ctx, tag):
+    """One verify block [a, g1, g2, random...] after the prompt: logits of every row within 1e-3
+    relative of the oracle's, the same per-row argmax, and the fused step's acceptance."""
+    cpu = cpu_model(m, max_ctx=max_ctx)
+    g = O.plain_greedy(cpu, prompt, 3)
+    cpu.reset()
+    vocab = LS.config_from_json(m["config_text"])["vocab"]
+    drafts = [g[1], g[2]] + rng.integers(0, vocab, k - 2).tolist()
+    block = [g[0]] + drafts
+    say(tag, "oracle")
+    cpu.forward(prompt)
+    ref = cpu.forward_multi(block, k + 1)
+    say(tag, "gpu")
+    gm = gpu_model(m, max_ctx=max_ctx)
+    assert gm.forward_argmax(prompt) == g[0]
+    p = gm.pos()
+    got = gm.forward_multi(block, k + 1)
+    rel = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    say(tag, "max rel logit diff", rel)
+    assert rel <= 1e-3
+    assert np.array_equal(got.argmax(1), ref.argmax(1))
+    gm.truncate(p)
+    acc, nxt = gm.verify_greedy(block)
+    want_m = 0
+    while want_m < k and ref[want_m].argmax() == drafts[want_m]:
+        want_m += 1
+    assert acc == want_m >= 2 and nxt == ref[want_m].argmax()
+
+
+def test_qwen3b_int8_verify_step_matches_the_oracle():
+    """The 3B shape (hidden 2048, head_dim 128, FFN 11008; the head's fragments exceed one
+    workgroup's LDS, so it runs as a split-K matrix launch), int8-g64, prompt of 64 ids, one
+    verify step of k=8."""
+    say("3B int8: build")
+    m = qwen3b((8, 64))
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, 151936, 64).tolist()
+    verify_step_vs_oracle(m, prompt, 8, rng, 256, "3B int8:")
+
+
+def test_qwen05b_int4_verify_step_after_a_long_prompt_matches_the_oracle():
+    """The int4-g32 configuration's shape with a 1100-token prompt (nine prefill chunks; the
+    verify rows attend over 69 blocks of 16 keys), one verify step of k=8."""
+    say("0.5B int4: build")
+    m = qwen05b((4, 32))
+    rng = np.random.default_rng(2048)
+    prompt = rng.integers(0, 151936, 1100).tolist()
+    verify_step_vs_oracle(m, prompt, 8, rng, 1200, "0.5B int4:")
