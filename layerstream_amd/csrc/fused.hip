@@ -257,8 +257,9 @@ void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, fl
 // ---------------------------------------------------------------------------------------
 // Main loop
 // ---------------------------------------------------------------------------------------
+// bf16 pair (a low, b high) of two floats that bf16 holds exactly: their high halves.
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-    return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xffff0000u);
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
 }
 
 // A operand (8 bf16) of k-step q of a chunk slot.
@@ -277,9 +278,17 @@ __device__ __forceinline__ uint4 a_operand(const uint4& raw, int q) {
         return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
     } else {
         const uint32_t d = q == 0 ? raw.x : (q == 1 ? raw.y : (q == 2 ? raw.z : raw.w));
+        // Nibbles hold value + 8; ((n + 0x78) ^ 0x80) is the value as a signed byte, four bytes
+        // at once (n + 0x78 <= 0x87, so no byte carries into the next). lo: values 0, 2, 4, 6;
+        // hi: values 1, 3, 5, 7.
+        const uint32_t lo = ((d & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
+        const uint32_t hi = (((d >> 4) & 0x0f0f0f0fu) + 0x78787878u) ^ 0x80808080u;
         float f[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) f[j] = float(int32_t((d >> (4 * j)) & 15u) - 8);
+        for (int b = 0; b < 4; b++) {
+            f[2 * b] = float(int32_t(lo << (24 - 8 * b)) >> 24);
+            f[2 * b + 1] = float(int32_t(hi << (24 - 8 * b)) >> 24);
+        }
         return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
     }
 }
