@@ -809,6 +809,7 @@ constexpr int head_pf() { return BITS == 4 ? (G16 ? 1 : 2) : 3; }
 template <bool G16>
 constexpr int head_waves() { return G16 ? 8 : 10; }
 constexpr int HEAD_WAVES_MAX = 10;
+constexpr int HEAD_BMAX = 16;  // fragment slots (16 B) copied to LDS per thread
 
 template <int BITS, bool G16>
 __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n_groups) {
@@ -829,22 +830,22 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     const int NC = W.n_chunks, F = my_groups * NC;
     const size_t sst = size_t(NC) * 1024;
     auto wbase = [&](int f) { return W.data + (size_t(4 * (first + (f / NC) * stride)) * NC * 64 + lane) * 16; };
+    // The tile's fragments (at most HEAD_BMAX per thread) are requested before the weight
+    // chunks: a wavefront's loads complete in order, so they reach LDS at L2 latency instead of
+    // waiting behind the HBM stream.
+    const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
+    const int nb = nks * 3 * 64, nthr = 64 * HEAD_WAVES;
+    uint4 bv[HEAD_BMAX];
+#pragma unroll
+    for (int u = 0; u < HEAD_BMAX; u++)
+        if (int(threadIdx.x) + u * nthr < nb) bv[u] = fb[threadIdx.x + u * nthr];
     uint4 raw[HEAD_PF][4];
 #pragma unroll
     for (int p = 0; p < HEAD_PF; p++)
         if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
-
-    const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
-    const int nb = nks * 3 * 64, nthr = 64 * HEAD_WAVES;
-    for (int i0 = threadIdx.x; i0 < nb; i0 += 8 * nthr) {
-        uint4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (i0 + u * nthr < nb) v[u] = fb[i0 + u * nthr];
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (i0 + u * nthr < nb) bl[i0 + u * nthr] = v[u];
-    }
+    for (int u = 0; u < HEAD_BMAX; u++)
+        if (int(threadIdx.x) + u * nthr < nb) bl[threadIdx.x + u * nthr] = bv[u];
     if (wv == 0) {
         if (a.ss) inv_rms(a, tile, W.cols, inv);
         else if (lane < FTOK) inv[lane] = 1.0f;
@@ -1122,7 +1123,9 @@ void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd
 
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES_MAX * FTOK * 8;
-    if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX) {
+    const int copy_slots = a.W.n_chunks * (tile_chunk_cols(a.W.bits) / 32) * 3 * 64;  // 16-byte fragment slots of a tile
+    const int min_threads = 64 * std::min(head_waves<true>(), head_waves<false>());
+    if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX || copy_slots > HEAD_BMAX * min_threads) {
         launch<EPI_HEAD, 4>(a, p, sc, s);
         return p.nrb;
     }
