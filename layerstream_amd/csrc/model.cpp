@@ -236,9 +236,9 @@ public:
         HIPC(hipStreamCreateWithFlags(&copy_, hipStreamNonBlocking));
         HIPC(hipStreamCreateWithFlags(&build_, hipStreamNonBlocking));
         const size_t rb = c_.row_bytes();
-        buf_size_ = std::max(L_.total, std::min(HEAD_ROWS, c_.vocab) * rb);
+        buf_size_ = std::max(L_.total, std::min(STREAM_HEAD_ROWS, c_.vocab) * rb);
         const Format ef = c_.embed_format;
-        hshape_ = tile_shape(ef.bits, ef.group, int(HEAD_ROWS), int(c_.hidden), 256);
+        hshape_ = tile_shape(ef.bits, ef.group, int(STREAM_HEAD_ROWS), int(c_.hidden), 256);
         slots_.resize(size_t(slots));
         for (auto& s : slots_) {
             s.raw = DevBuf(buf_size_);
@@ -291,10 +291,10 @@ public:
         return cur_layer_;
     }
     void release_layer(size_t) override { release(); }
-    size_t n_head_chunks() const override { return (c_.vocab + HEAD_ROWS - 1) / HEAD_ROWS; }
+    size_t n_head_chunks() const override { return (c_.vocab + STREAM_HEAD_ROWS - 1) / STREAM_HEAD_ROWS; }
     HeadChunk head_chunk(size_t c) override {
         Slot& s = take({HEAD, c});
-        const size_t first = c * HEAD_ROWS, rows = std::min(HEAD_ROWS, c_.vocab - first);
+        const size_t first = c * STREAM_HEAD_ROWS, rows = std::min(STREAM_HEAD_ROWS, c_.vocab - first);
         TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
         m.rows = int(rows);
         return HeadChunk{first, rows, m};
@@ -337,8 +337,8 @@ private:
         if (it.kind == LAYER) {
             bytes = L_.total;
         } else {
-            first = it.idx * HEAD_ROWS;
-            rows = std::min(HEAD_ROWS, c_.vocab - first);
+            first = it.idx * STREAM_HEAD_ROWS;
+            rows = std::min(STREAM_HEAD_ROWS, c_.vocab - first);
             bytes = rows * rb;
         }
         const uint8_t* from;
@@ -486,8 +486,8 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if ((c.heads + c.kv_heads) * c.head_dim % 16) fail("q and k heads must fill whole 16-row strips");
     {
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
-        const size_t n_chunks = (c.vocab + HEAD_ROWS - 1) / HEAD_ROWS;
-        head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * HEAD_ROWS / 64));
+        const size_t n_chunks = (c.vocab + STREAM_HEAD_ROWS - 1) / STREAM_HEAD_ROWS;
+        head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * STREAM_HEAD_ROWS / 64));
     }
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
@@ -507,7 +507,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const LayerArena la = layer_arena(c);
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const int n = int(T);
-        const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(HEAD_ROWS), int(h), 256);
+        const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(STREAM_HEAD_ROWS), int(h), 256);
         const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1),        mm_plan(la.o, 1, kw_o_, n, 1),
                                 gu_plan(la.gu, kw_gu_, n), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS),
                                 mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};

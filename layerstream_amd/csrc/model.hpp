@@ -73,6 +73,10 @@ struct HeadChunk {
 };
 
 constexpr size_t HEAD_ROWS = 4096;  // src/provider.rs:21
+// Streamed table pieces: four of the reference's chunks per copy (about a layer block at int4), so
+// the table crosses PCIe in 10 copies instead of 38. Every logit depends on its own row only, so
+// the piece size changes no value.
+constexpr size_t STREAM_HEAD_ROWS = 4 * HEAD_ROWS;
 
 class DeviceProvider {
 public:
