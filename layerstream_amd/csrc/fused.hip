@@ -755,10 +755,26 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     }
 }
 
+// Workgroup -> (row block and split, token tile) of a launch over several tiles. Workgroups go
+// to the 8 XCDs in turn (dispatch index L to XCD L % 8); each XCD gets a contiguous run of
+// (row block, tile) pairs, row block major, so the tiles of one row block run side by side on
+// one XCD and all but the first read its weights from that XCD's L2. Any order gives the same
+// bits: only which workgroup computes a piece changes.
+__device__ __forceinline__ void xcd_tile_map(int& bx, int& tile) {
+    const int tiles = gridDim.y, G = gridDim.x * tiles;
+    const int L = blockIdx.x + blockIdx.y * gridDim.x;
+    const int x = L % 8, k = L / 8, base = G / 8, rem = G % 8;
+    const int P = x * base + min(x, rem) + k;
+    bx = P / tiles;
+    tile = P % tiles;
+}
+
 template <int BITS, int EPI, bool G16, int S>
 __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     extern __shared__ __align__(16) uint8_t smem[];
-    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, blockIdx.x, blockIdx.y, smem);
+    int bx = blockIdx.x, tile = blockIdx.y;
+    if (gridDim.y > 1) xcd_tile_map(bx, tile);
+    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, bx, tile, smem);
 }
 
 // gate|up and down in one launch (one token tile): workgroups [0, n_gu) run gate|up and count
@@ -817,7 +833,9 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int Q = Steps<BITS>::Q, HEAD_PF = head_pf<BITS, G16>();
     const TMat& W = a.W;
-    const int tile = blockIdx.y, lane = threadIdx.x & 63;
+    int bx = blockIdx.x, tile = blockIdx.y;
+    if (gridDim.y > 1) xcd_tile_map(bx, tile);  // a block's tiles side by side on one XCD
+    const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nt = min(FTOK, a.n - tile * FTOK), ibase = tile * FTOK;
     const int nks = W.n_chunks * Q;
@@ -825,7 +843,7 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     float* inv = reinterpret_cast<float*>(smem + size_t(nks) * 3 * 1024);
 
     // This wavefront's groups: g = first + k * stride. Its first weight chunks go out at once.
-    const int stride = gridDim.x * HEAD_WAVES, first = blockIdx.x * HEAD_WAVES + wv;
+    const int stride = gridDim.x * HEAD_WAVES, first = bx * HEAD_WAVES + wv;
     const int my_groups = first < n_groups ? (n_groups - first + stride - 1) / stride : 0;
     const int NC = W.n_chunks, F = my_groups * NC;
     const size_t sst = size_t(NC) * 1024;
@@ -927,7 +945,7 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
                 v = wv_v[w * FTOK + tok];
                 ix = wv_i[w * FTOK + tok];
             }
-        const size_t at = (size_t(tile) * a.arg_stride + a.arg_off + blockIdx.x) * FTOK + tok;
+        const size_t at = (size_t(tile) * a.arg_stride + a.arg_off + bx) * FTOK + tok;
         a.arg_val[at] = v;
         a.arg_idx[at] = ix;
     }
