@@ -114,6 +114,36 @@ __device__ __forceinline__ void attn_load(AttnBlock<HD>& r, int b, int last_key,
     }
 }
 
+// attn_load through the coherent path, for key rows written earlier in the same launch: rk and
+// rv cover the caches from kc / vc.
+template <int HD>
+__device__ __forceinline__ void attn_load_coherent(AttnBlock<HD>& r, int b, int last_key, __amdgpu_buffer_rsrc_t rk,
+                                                   __amdgpu_buffer_rsrc_t rv, int kv, int col0, int g, int c) {
+    constexpr int H4 = HD / 4, DB = HD / 16;
+    const int key = AKB * b + c;
+#pragma unroll
+    for (int j = 0; j < H4; j += 4) {
+        const attn_f32x4 x = key <= last_key ? ld_attn_f32x4(rk, (key * kv + col0 + g * H4 + j) * 4) : attn_f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 4; e++) r.k[j + e] = x[e];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int vk = AKB * b + 4 * g + u;
+        if constexpr (DB % 4 == 0) {
+#pragma unroll
+            for (int db = 0; db < DB; db += 4) {
+                const attn_f32x4 x = vk <= last_key ? ld_attn_f32x4(rv, (vk * kv + col0 + DB * c + db) * 4) : attn_f32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 4; e++) r.v[u * DB + db + e] = x[e];
+            }
+        } else {
+#pragma unroll
+            for (int db = 0; db < DB; db++) r.v[u * DB + db] = vk <= last_key ? ld_f32(rv, (vk * kv + col0 + DB * c + db) * 4) : 0.0f;
+        }
+    }
+}
+
 // The arguments of one attention launch (see attention() in kernels.hpp); pm, pl, po are the
 // per-workgroup states in the scratch buffer.
 struct AttnArgs {
@@ -154,8 +184,11 @@ inline AttnArgs make_attn_args(const float* q, int ldq, int t, int heads, int kv
 
 // Workgroup s of (head, segment seg) (256 threads). With OUT_FLOW the output fragments are
 // written through the coherent path and the merging workgroup then signals fl (producer 0).
-template <int HD, bool OUT_FLOW>
-__device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, int seg, const Flow& fl) {
+// With IN_FLOW (one sequence) q and the keys from the launch's first position on are written by
+// earlier workgroups of the same launch: the workgroup loads its first block if it holds only
+// older keys, waits on fin (counter `head`), then reads q and newer keys coherently.
+template <int HD, bool OUT_FLOW, bool IN_FLOW = false>
+__device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, int seg, const Flow& fl, const Flow& fin = Flow{}) {
     const float* __restrict__ q = A.q;
     const int ldq = A.ldq, t = A.t, heads = A.heads, kv_heads = A.kv_heads;
     const AttnRows& rows = A.rows;
@@ -197,9 +230,27 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(po, rows_total * ASPLIT * HD * 4);
 
     AttnBlock<HD> ba, bb;
-    if (first < nb) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
     float qr[H4];
-    {
+    // Blocks below nold hold only keys cached before this launch (every block without IN_FLOW).
+    const int nold = IN_FLOW ? *A.pos0p / AKB : nb;
+    const __amdgpu_buffer_rsrc_t rk = coherent_rsrc(kc, size_t(last_key + 1) * kv * 4);
+    const __amdgpu_buffer_rsrc_t rv = coherent_rsrc(vc, size_t(last_key + 1) * kv * 4);
+    auto load_block = [&](AttnBlock<HD>& r, int b) {
+        if (IN_FLOW && b >= nold) attn_load_coherent<HD>(r, b, last_key, rk, rv, kv, col0, g, c);
+        else attn_load<HD>(r, b, last_key, kc, vc, kv, col0, g, c);
+    };
+    if (first < nb && first < nold) load_block(ba, first);
+    if constexpr (IN_FLOW) {
+        flow_wait(fin, head);
+        if (first < nb && first >= nold) load_block(ba, first);
+        const __amdgpu_buffer_rsrc_t rq = coherent_rsrc(q, size_t(t) * ldq * 4);
+#pragma unroll
+        for (int j = 0; j < H4; j += 4) {
+            const attn_f32x4 x = c < nq ? ld_attn_f32x4(rq, ((i0 + c) * ldq + head * HD + g * H4 + j) * 4) : attn_f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 4; e++) qr[j + e] = x[e];
+        }
+    } else {
         const float* qp = q + size_t(i0 + c) * ldq + head * HD + g * H4;
 #pragma unroll
         for (int j = 0; j < H4; j += 4) {
@@ -251,10 +302,10 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         }
     };
     for (int b = first; b < nb; b += 2 * stride) {
-        if (b + stride < nb) attn_load<HD>(bb, b + stride, last_key, kc, vc, kv, col0, g, c);
+        if (b + stride < nb) load_block(bb, b + stride);
         block(b, ba);
         if (b + stride >= nb) break;
-        if (b + 2 * stride < nb) attn_load<HD>(ba, b + 2 * stride, last_key, kc, vc, kv, col0, g, c);
+        if (b + 2 * stride < nb) load_block(ba, b + 2 * stride);
         block(b + stride, bb);
     }
 

@@ -77,7 +77,7 @@ constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
 __device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
     if (threadIdx.x == 0) {
         int* cnt = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + j);
-        const int want = min(fl.producers, fl.per * (j + 1)) - fl.per * j;
+        const int want = fl.want > 0 ? fl.want : min(fl.producers, fl.per * (j + 1)) - fl.per * j;
         int zero = 0;
         asm volatile("" : "+v"(zero));
         unsigned spins = 0;
@@ -98,13 +98,33 @@ __device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
 }
 
 // Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
-// moves.
+// moves. (qkv_signal below is the producer side for q|k|v -> attention.)
 __device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
         __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + r / fl.per), 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// q|k|v strip r (16 rows: q heads, then k heads, then v heads, hd / 16 strips each) is stored:
+// count it for every head that reads it, counter base + head (a q strip: its head; a k or v
+// strip: the heads of its group).
+__device__ __forceinline__ void qkv_signal(const Flow& fl, int r, int heads, int kv_heads, int hd) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    const int sph = hd / 16, qs = heads * sph, ks = kv_heads * sph, group = heads / kv_heads;
+    int h0 = 0, nh = 0;
+    if (r < qs) {
+        h0 = r / sph;
+        nh = 1;
+    } else if (r < qs + 2 * ks) {
+        h0 = ((r - qs) % ks) / sph * group;
+        nh = group;
+    }
+    for (int h = h0; h < h0 + nh; h++)
+        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + h), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace ls

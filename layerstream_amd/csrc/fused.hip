@@ -629,7 +629,11 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
 
     if constexpr (EPI == EPI_QKV) {
         // Tile rows: q heads, k heads (RoPE pairs adjacent), v heads (src/kernels.rs:242-252).
+        // With OUT_FLOW the rows go through the coherent path for this launch's attention.
         const int hd = a.hd, half = hd / 2, h = a.heads * hd, kvd = a.kv_heads * hd;
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kcache, 0, 0x7ffffffc, BUF_DWORD3);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vcache, 0, 0x7ffffffc, BUF_DWORD3);
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
             if (tok >= nt || row >= W.rows) continue;
@@ -649,10 +653,17 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                     ref = row - r + half + j;
                 }
             }
-            if (ref < h) a.out[size_t(i) * a.ldo + ref] = v;
-            else if (ref < h + kvd) a.kcache[size_t(crow) * kvd + (ref - h)] = v;
-            else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
+            if constexpr (OUT_FLOW) {
+                if (ref < h) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rq, (i * a.ldo + ref) * 4, 0, CPOL_SC1);
+                else if (ref < h + kvd) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rk, (crow * kvd + ref - h) * 4, 0, CPOL_SC1);
+                else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rv, (crow * kvd + ref - h - kvd) * 4, 0, CPOL_SC1);
+            } else {
+                if (ref < h) a.out[size_t(i) * a.ldo + ref] = v;
+                else if (ref < h + kvd) a.kcache[size_t(crow) * kvd + (ref - h)] = v;
+                else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
+            }
         }
+        if constexpr (OUT_FLOW) qkv_signal(fl, rb, a.heads, a.kv_heads, a.hd);
     } else if constexpr (EPI == EPI_RESID) {
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
             const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
@@ -810,6 +821,27 @@ __global__ __launch_bounds__(512) void k_attn_o(AttnArgs aa, MMArgs o, MMPlan po
     } else {
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
         mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fl, int(blockIdx.x) - na, 0, smem);
+    }
+}
+
+// q|k|v, attention and o in one launch (one token tile): workgroups [0, nq) are the q|k|v strips
+// (producers of the per-head counters), then ASPLIT per head run attention (consumers of their
+// head's counter, producers of the o counter), then the o workgroups. Every workgroup waits only
+// for workgroups with lower indices, which are dispatched before it.
+template <int HD, int BITS, bool G16>
+__global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnArgs aa, MMArgs o, MMPlan po, MMScratch sc, Flow fq,
+                                                    Flow fo) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nq = pq.nrb * pq.nsplit, na = ASPLIT * aa.heads, bid = blockIdx.x;
+    if (bid < nq) {
+        if (int(threadIdx.x) >= 64 * pq.rg * pq.kw) return;
+        mm_body<BITS, EPI_QKV, G16, 1, false, true>(qa, pq, sc, fq, bid, 0, smem);
+    } else if (bid < nq + na) {
+        if (int(threadIdx.x) >= AWV * 64) return;
+        attn_body<HD, true, true>(aa, (bid - nq) % ASPLIT, (bid - nq) / ASPLIT, 0, fo, fq);
+    } else {
+        if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
+        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fo, bid - nq - na, 0, smem);
     }
 }
 
@@ -1135,6 +1167,63 @@ void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd
         case 32: launch_attn_o<32>(aa, o, po, sc, fl, s); break;
         case 64: launch_attn_o<64>(aa, o, po, sc, fl, s); break;
         case 128: launch_attn_o<128>(aa, o, po, sc, fl, s); break;
+        default: throw std::runtime_error("head_dim must be 16, 32, 64 or 128");
+    }
+}
+
+int qkv_attention_o_workgroups(int heads, const MMPlan& pq, const MMPlan& po) {
+    return pq.nrb * pq.nsplit + ASPLIT * heads + po.nrb * po.nsplit;
+}
+
+template <int HD>
+static void launch_qkv_attn_o(const MMArgs& qa, const MMPlan& pq, const AttnArgs& aa, const MMArgs& o, const MMPlan& po, const MMScratch& sc,
+                              const Flow& fq, const Flow& fo, hipStream_t s) {
+    const dim3 grid(qkv_attention_o_workgroups(aa.heads, pq, po)), block(std::max({AWV * 64, 64 * po.rg * po.kw, 64 * pq.rg * pq.kw}));
+    const size_t lds = std::max(lds_bytes(pq), lds_bytes(po));
+    const bool g16 = o.W.bits != 16 && o.W.group == 16;
+    switch (o.W.bits) {
+        case 16: go(k_qkv_attn_o<HD, 16, false>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo); break;
+        case 8:
+            if (g16) go(k_qkv_attn_o<HD, 8, true>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo);
+            else go(k_qkv_attn_o<HD, 8, false>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo);
+            break;
+        default:
+            if (g16) go(k_qkv_attn_o<HD, 4, true>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo);
+            else go(k_qkv_attn_o<HD, 4, false>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo);
+            break;
+    }
+    FCHECK(hipGetLastError());
+}
+
+void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cnt, uint8_t* frags, const MMArgs& o, const MMPlan& po,
+                     const MMScratch& sc, int* ctl, hipStream_t s) {
+    const int heads = qa.heads, kvh = qa.kv_heads, hd = qa.hd, t = qa.n;
+    if (t > FTOK || pq.tiles != 1 || po.tiles != 1) throw std::runtime_error("the fused q|k|v/attention/o launch takes one token tile");
+    if (pq.s != 1 || pq.rg != 1 || pq.nsplit != 1) throw std::runtime_error("the fused launch needs q|k|v as one workgroup per strip");
+    if (po.s != 1 || po.nsplit != 1) throw std::runtime_error("the fused launch needs o without a K split");
+    if (64 * po.rg * po.kw > 512 || 64 * pq.kw > 512) throw std::runtime_error("workgroups too large for the fused launch");
+    if (heads > FLOW_ATTN_O || hd % 16 || heads % kvh) throw std::runtime_error("heads do not fit the fused launch's counters");
+    if (hd / 2 > ROPE_HALF_MAX || (heads + kvh) * hd % 16) throw std::runtime_error("head_dim must be even and at most 256");
+    const AttnArgs aa = make_attn_args(qa.out, qa.ldo, t, heads, kvh, hd, qa.pos0, AttnRows{}, qa.kcache, qa.vcache, scratch, cnt, frags);
+    // q|k|v -> attention: counter h (h < heads) counts the q strips of head h and the k and v
+    // strips of its group.
+    Flow fq;
+    fq.ctl = ctl;
+    fq.producers = pq.nrb;
+    fq.want = 3 * (hd / 16);
+    fq.consumers = ASPLIT;
+    fq.base = 0;
+    Flow fo;
+    fo.ctl = ctl;
+    fo.producers = heads;
+    fo.per = heads;
+    fo.consumers = po.nrb * po.nsplit;
+    fo.base = FLOW_ATTN_O;
+    switch (hd) {
+        case 16: launch_qkv_attn_o<16>(qa, pq, aa, o, po, sc, fq, fo, s); break;
+        case 32: launch_qkv_attn_o<32>(qa, pq, aa, o, po, sc, fq, fo, s); break;
+        case 64: launch_qkv_attn_o<64>(qa, pq, aa, o, po, sc, fq, fo, s); break;
+        case 128: launch_qkv_attn_o<128>(qa, pq, aa, o, po, sc, fq, fo, s); break;
         default: throw std::runtime_error("head_dim must be 16, 32, 64 or 128");
     }
 }

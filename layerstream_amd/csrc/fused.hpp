@@ -150,10 +150,12 @@ struct Flow {
     int per = 1;        // producers per counter
     int consumers = 0;  // consumer workgroups per counter
     int base = 0;       // first counter of this launch
+    int want = 0;       // when set: the count every counter waits for (producers may feed several)
 };
 // Control block words: error flag, greedy acceptance (m, next), then the counters (gate|up ->
-// down from counter 0, attention -> o at FLOW_ATTN_O).
-enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 16, FLOW_ATTN_O = FLOW_COUNTERS - 1 };
+// down from counter 0; q|k|v -> attention one per head from counter 0; attention -> o at
+// FLOW_ATTN_O).
+enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 32, FLOW_ATTN_O = FLOW_COUNTERS - 1 };
 constexpr int FLOW_WORDS = FLOW_CNT0 + FLOW_CNT_STRIDE * FLOW_COUNTERS;
 
 // QKV projection + 1/rms + bias + RoPE + K/V append (plan strips 1). Rows: q heads and k heads
@@ -179,6 +181,16 @@ void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd
                  hipStream_t s);
 // Workgroups of an attention_o launch (its grid, one workgroup per CU at most).
 int attention_o_workgroups(int heads, const MMPlan& po);
+// q|k|v (mm_qkv, plan strips 1 without a K split: one workgroup per 16-row strip), attention and
+// o in one launch for one token tile: q|k|v rows are stored through the coherent path and each
+// strip counts itself done for the heads that read it (a q strip for its head, a k or v strip for
+// every head of its group); the attention workgroups load the keys and values cached before this
+// pass while q|k|v runs, wait for their head, then read q and the new rows coherently; o as in
+// attention_o. q, the caches and the position come from qa.
+void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cnt, uint8_t* frags, const MMArgs& o, const MMPlan& po,
+                     const MMScratch& sc, int* ctl, hipStream_t s);
+// Workgroups of a qkv_attention_o launch.
+int qkv_attention_o_workgroups(int heads, const MMPlan& pq, const MMPlan& po);
 
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
 // partials at [tile][arg_off + b][16] for b below the returned count.

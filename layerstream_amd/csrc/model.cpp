@@ -491,6 +491,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     }
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
+    if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -683,8 +684,9 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
         float* kc = kcache_.as<float>() + cache_off;
         float* vc = vcache_.as<float>() + cache_off;
         if (!res) x_frags(x, T, h, L.in_norm, xf, ss, s);
+        MMArgs qa;
         {
-            MMArgs a;
+            MMArgs& a = qa;
             a.W = L.qkv;
             a.frags = xf;
             a.frag_stride = fb_h_;
@@ -708,10 +710,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.heads = heads;
             a.kv_heads = kvh;
             a.hd = hd;
-            prof_begin();
-            mm_qkv(a, mm_plan(L.qkv, 1, kw_qkv_, T, 1), scr, s);
-            prof_end(L.qkv, T);
         }
+        const MMPlan pq = mm_plan(L.qkv, 1, kw_qkv_, T, 1);
         {
             MMArgs a;
             a.W = L.o;
@@ -727,14 +727,30 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.oss_slots = slots_h_;
             const MMPlan po = mm_plan(L.o, 1, kw_o_, T, 1);
             // One launch for attention and o when the o workgroups can fetch their weights while
-            // attention runs (one token tile, every workgroup resident at once).
-            if (fuse_on_ && !bv && po.tiles == 1 && po.nsplit == 1 && 64 * po.rg * po.kw <= 512 &&
-                attention_o_workgroups(heads, po) <= device_cu_count()) {
+            // attention runs (one token tile, every workgroup resident at once); q|k|v joins it
+            // when it runs as one workgroup per strip, and attention then fetches the cached
+            // keys and values while q|k|v runs.
+            const bool fuse_ao = fuse_on_ && !bv && po.tiles == 1 && po.nsplit == 1 && 64 * po.rg * po.kw <= 512 &&
+                                 attention_o_workgroups(heads, po) <= device_cu_count();
+            const bool fuse_qao = fuse_ao && fuse_qkv_ && pq.s == 1 && pq.rg == 1 && pq.nsplit == 1 && 64 * pq.kw <= 512 &&
+                                  heads <= FLOW_ATTN_O && qkv_attention_o_workgroups(heads, pq, po) <= device_cu_count();
+            if (fuse_qao) {
+                prof_begin();
+                qkv_attention_o(qa, pq, attn_scratch_.as<float>(), attn_cnt_.as<int>(), af_.as<uint8_t>(), a, po, scr, ctl_.as<int>(), s);
+                prof_end(L.qkv, T);
+                prof_end(L.o, T, false, 2.0 * kv * 4 * double(pos_ + T));  // + the K/V rows attention reads
+            } else if (fuse_ao) {
+                prof_begin();
+                mm_qkv(qa, pq, scr, s);
+                prof_end(L.qkv, T);
                 prof_begin();
                 attention_o(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, kc, vc, attn_scratch_.as<float>(), attn_cnt_.as<int>(),
                             af_.as<uint8_t>(), a, po, scr, ctl_.as<int>(), s);
                 prof_end(L.o, T, true, 2.0 * kv * 4 * double(pos_ + T));  // + the K/V rows attention reads
             } else {
+                prof_begin();
+                mm_qkv(qa, pq, scr, s);
+                prof_end(L.qkv, T);
                 attention(q_.as<float>(), hq, T, heads, kvh, hd, pos_dev, bv ? bv->attn : AttnRows{}, kc, vc, attn_scratch_.as<float>(),
                           attn_cnt_.as<int>(), af_.as<uint8_t>(), s);
                 prof_begin();
