@@ -533,7 +533,16 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         }
     }
     if constexpr (IN_FLOW) {
-        // The weights are in flight; wait for the input, then read it coherently.
+        // The weights are in flight; touch this workgroup's share of the prefetch range (1 KiB
+        // per wavefront load, into LDS that the reduction overwrites later), wait for the input,
+        // then read it coherently.
+        if (a.pf) {
+            const size_t nwg = size_t(p.nrb) * p.nsplit, per = (a.pf_bytes / nwg + 1023) / 1024 * 1024;
+            const size_t beg = size_t(bx) * per, end = min(a.pf_bytes, beg + per);
+            auto* lds = (__attribute__((address_space(3))) void*)(smem + size_t(wv) * 1024);
+            for (size_t off = beg + size_t(wv) * 1024; off < end; off += size_t(nw) * 1024)
+                if (off + size_t(lane) * 16 + 16 <= end) __builtin_amdgcn_global_load_lds(a.pf + off + lane * 16, lds, 16, 0, 0);
+        }
         flow_wait(fl, sp);
         const __amdgpu_buffer_rsrc_t rf =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.frags) + size_t(tile) * a.frag_stride, 0, int(a.frag_stride), BUF_DWORD3);

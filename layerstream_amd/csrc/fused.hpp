@@ -113,6 +113,10 @@ struct MMArgs {
     int arg_stride = 0, arg_off = 0;
     int row_base = 0;       // added to argmax row indices
     float* row0 = nullptr;  // logits of row 0 per token ([tile * 16 + token]), when set
+    // Consumers of a fused launch: bytes to read (into LDS, discarded) while waiting for the
+    // input, so that a later launch finds them in the memory-side cache.
+    const uint8_t* pf = nullptr;
+    size_t pf_bytes = 0;
 };
 
 // Work split of one launch: each wavefront streams s strips (16 s rows); a workgroup owns rg

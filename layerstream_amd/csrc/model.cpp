@@ -492,6 +492,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
+    if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -734,6 +735,14 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                                  attention_o_workgroups(heads, po) <= device_cu_count();
             const bool fuse_qao = fuse_ao && fuse_qkv_ && pq.s == 1 && pq.rg == 1 && pq.nsplit == 1 && 64 * pq.kw <= 512 &&
                                   heads <= FLOW_ATTN_O && qkv_attention_o_workgroups(heads, pq, po) <= device_cu_count();
+            if (pf_on_) {
+                // While waiting for attention, the o workgroups read this layer's gate|up and
+                // down weights once, so that their launch finds them in the memory-side cache.
+                const uint8_t* end = L.down.scales ? reinterpret_cast<const uint8_t*>(L.down.scales) + tile_scale_bytes(L.down)
+                                                   : L.down.data + tile_data_bytes(L.down);
+                a.pf = L.gu.data;
+                a.pf_bytes = size_t(end - L.gu.data);
+            }
             if (fuse_qao) {
                 prof_begin();
                 qkv_attention_o(qa, pq, attn_scratch_.as<float>(), attn_cnt_.as<int>(), af_.as<uint8_t>(), a, po, scr, ctl_.as<int>(), s);
@@ -783,6 +792,15 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 d.onorm = last ? fnorm_.as<float>() : prov_->layer(l + 1).in_norm;
                 d.oss = ss;
                 d.oss_slots = slots_h_;
+            }
+            if (pf_on_ && res && !last) {
+                // While waiting for gate|up, the down workgroups read the next layer's q|k|v and
+                // o weights once (resident layers: already in place).
+                const DevLayer& N = prov_->layer(l + 1);
+                const uint8_t* end = N.o.scales ? reinterpret_cast<const uint8_t*>(N.o.scales) + tile_scale_bytes(N.o)
+                                                : N.o.data + tile_data_bytes(N.o);
+                d.pf = N.qkv.data;
+                d.pf_bytes = size_t(end - N.qkv.data);
             }
             const MMPlan pg = gu_plan(L.gu, kw_gu_, T), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS);
             // Fused only when both roles fit on the device at one workgroup per CU (their

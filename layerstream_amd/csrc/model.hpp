@@ -177,6 +177,7 @@ private:
     static constexpr int CTL_BACK = FLOW_ACC + 2;  // control words copied back after a pass: error, acceptance
     bool fuse_on_ = true;
     bool fuse_qkv_ = true;  // q|k|v joins the attention + o launch
+    bool pf_on_ = true;     // fused consumers prefetch the next launch's weights
     const int* stage_pos_ = nullptr;  // device positions of the staged chunks
     size_t vpad_ = 0, fb_h_ = 0, fb_q_ = 0, fb_in_ = 0;
     int head_blocks_ = 0, slots_h_ = 0;
