@@ -241,7 +241,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     };
     if (first < nb && first < nold) load_block(ba, first);
     if constexpr (IN_FLOW) {
-        flow_wait(fin, head);
+        flow_wait(fin, head, s);
         if (first < nb && first >= nold) load_block(ba, first);
         const __amdgpu_buffer_rsrc_t rq = coherent_rsrc(q, size_t(t) * ldq * 4);
 #pragma unroll

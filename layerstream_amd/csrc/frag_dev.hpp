@@ -74,42 +74,57 @@ __device__ __forceinline__ void write_slot_coherent(__amdgpu_buffer_rsrc_t r, si
 // the wait records an error and goes on, so every wave ends.
 constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
 
-__device__ __forceinline__ void flow_wait(const Flow& fl, int j) {
+// A flow without a control block (a stage whose input was written before the launch) does not
+// wait. Every 64 polls the wait also reads the error word, so that once one wait of a launch
+// has given up, the others stop waiting at once and the launch drains.
+// Consumer `who` (0, 1, ... among the counter's consumers) polls copy who % mirrors.
+__device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
+    if (!fl.ctl) return;
     if (threadIdx.x == 0) {
-        int* cnt = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + j);
+        int* c0 = fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + j * fl.mirrors);
+        int* cnt = c0 + FLOW_CNT_STRIDE * (who % fl.mirrors);
         const int want = fl.want > 0 ? fl.want : min(fl.producers, fl.per * (j + 1)) - fl.per * j;
         int zero = 0;
         asm volatile("" : "+v"(zero));
         unsigned spins = 0;
+#ifdef LS_POLL_LOAD
+        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(cnt, 0, 4, BUF_DWORD3);
+        while (int(__builtin_amdgcn_raw_buffer_load_b32(rc, 0, 0, CPOL_SC1)) < want) {
+#else
         while (__hip_atomic_fetch_add(cnt, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
+#endif
             if (++spins > FLOW_SPIN_LIMIT) {
                 __hip_atomic_store(fl.ctl + FLOW_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
+            if ((spins & 63) == 0 && __hip_atomic_fetch_add(fl.ctl + FLOW_ERR, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                break;
             __builtin_amdgcn_s_sleep(2);
         }
-        const int old = __hip_atomic_fetch_add(cnt + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(c0 + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == fl.consumers - 1) {
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int m = 0; m < fl.mirrors; m++) __hip_atomic_store(c0 + FLOW_CNT_STRIDE * m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(c0 + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
     __syncthreads();
 }
 
 // Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
-// moves. (qkv_signal below is the producer side for q|k|v -> attention.)
+// moves. A flow without a control block has no consumers in this launch: nothing to signal.
+// (qkv_signal below is the producer side for q|k|v -> attention.)
 __device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
+    if (!fl.ctl) return;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + r / fl.per), 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    if (int(threadIdx.x) < fl.mirrors)
+        __hip_atomic_fetch_add(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.base + (r / fl.per) * fl.mirrors + int(threadIdx.x)), 1,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // q|k|v strip r (16 rows: q heads, then k heads, then v heads, hd / 16 strips each) is stored:
 // count it for every head that reads it, counter base + head (a q strip: its head; a k or v
-// strip: the heads of its group).
+// strip: the heads of its group). These counters have one copy (ATTN_SPLIT consumers each).
 __device__ __forceinline__ void qkv_signal(const Flow& fl, int r, int heads, int kv_heads, int hd) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();

@@ -383,18 +383,30 @@ enum { EPI_QKV = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_HEAD = 3 };
 struct RmsLoads {
     float x[16];
 };
+// With COH the partials were written earlier in the same launch and are read through the
+// coherent path.
+template <bool COH = false>
+__device__ __forceinline__ float ss_load(const MMArgs& a, int tile, int sl, int tok) {
+    if constexpr (COH) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ss) + size_t(tile) * a.ss_slots * FTOK, 0,
+                                                                          a.ss_slots * FTOK * 4, BUF_DWORD3);
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (sl * FTOK + tok) * 4, 0, CPOL_SC1));
+    } else {
+        return a.ss[(size_t(tile) * a.ss_slots + sl) * FTOK + tok];
+    }
+}
+template <bool COH = false>
 __device__ __forceinline__ void rms_issue(const MMArgs& a, int tile, RmsLoads& r) {
     const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
-    const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const int sl = part + 4 * k;
-        r.x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
+        r.x[k] = sl < a.ss_slots ? ss_load<COH>(a, tile, sl, tok) : 0.0f;
     }
 }
+template <bool COH = false>
 __device__ __forceinline__ void rms_finish(const MMArgs& a, int tile, int cols, const RmsLoads& r, float* inv) {
     const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
-    const float* sb = a.ss + size_t(tile) * a.ss_slots * FTOK + tok;
     float v = 0.0f;
 #pragma unroll
     for (int k = 0; k < 16; k++) v += r.x[k];
@@ -403,7 +415,7 @@ __device__ __forceinline__ void rms_finish(const MMArgs& a, int tile, int cols, 
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const int sl = part + 4 * (k0 + k);
-            x[k] = sl < a.ss_slots ? sb[sl * FTOK] : 0.0f;
+            x[k] = sl < a.ss_slots ? ss_load<COH>(a, tile, sl, tok) : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < 16; k++) v += x[k];
@@ -442,12 +454,14 @@ constexpr int ROPE_HALF_MAX = 128;
 // 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half, per-token position and
 // cache row 2 x 16].
 // One matrix workgroup (row block bx / nsplit, K range bx % nsplit, token tile `tile`). With
-// IN_FLOW the input fragments come from earlier workgroups of the same launch: they are read
-// through the coherent path after waiting on fl. With OUT_FLOW (SiLU epilogue) the output
-// fragments are written through the coherent path and the workgroup then signals its counter.
+// IN_FLOW the input (fragments, and the sum-of-squares partials of a normalised input) comes
+// from earlier workgroups of the same launch: it is read through the coherent path after
+// waiting on fin. With OUT_FLOW the outputs are written through the coherent path and the
+// workgroup then signals fout; for the residual epilogue the residual rows themselves were
+// written in the same launch, so they too are read coherently after the wait.
 template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false>
-__device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const MMScratch& sc, const Flow& fl, int bx, int tile,
-                                        uint8_t* smem) {
+__device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const MMScratch& sc, const Flow& fin, const Flow& fout, int bx,
+                                        int tile, uint8_t* smem) {
     constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
     const int nw = p.rg * p.kw, nthr = nw * 64;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -498,10 +512,16 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     // Sum-of-squares partials for 1 / rms (wavefront 0), in flight with the weights.
     RmsLoads rms;
     const bool do_rms = a.ss && wv == 0;
-    if (do_rms) rms_issue(a, tile, rms);
+    if (do_rms && !IN_FLOW) rms_issue(a, tile, rms);
+    // Residual rows written in this launch (coherent residual epilogue): XR per thread, loaded
+    // after the wait.
+    constexpr bool XCOH = EPI == EPI_RESID && OUT_FLOW;
+    static_assert(!XCOH || IN_FLOW, "a residual epilogue with in-launch consumers also has an in-launch input");
+    constexpr int XR = 4;  // the host checks 16 S rg x 16 <= XR x 64 rg kw (S <= kw)
+    float xr[XR];
     // Epilogue operands, staged in LDS while the weights are in flight.
     if constexpr (EPI == EPI_RESID) {
-        for (int e0 = threadIdx.x; e0 < rows_wg * FTOK; e0 += 4 * nthr) {
+        for (int e0 = threadIdx.x; !XCOH && e0 < rows_wg * FTOK; e0 += 4 * nthr) {
             float xv[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -543,7 +563,18 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             for (size_t off = beg + size_t(wv) * 1024; off < end; off += size_t(nw) * 1024)
                 if (off + size_t(lane) * 16 + 16 <= end) __builtin_amdgcn_global_load_lds(a.pf + off + lane * 16, lds, 16, 0, 0);
         }
-        flow_wait(fl, sp);
+        flow_wait(fin, sp, rb);
+        if (do_rms) rms_issue<true>(a, tile, rms);
+        if constexpr (XCOH) {
+            const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
+#pragma unroll
+            for (int u = 0; u < XR; u++) {
+                const int e = threadIdx.x + u * nthr, rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+                xr[u] = (e < rows_wg * FTOK && tok < nt && row < W.rows)
+                            ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1))
+                            : 0.0f;
+            }
+        }
         const __amdgpu_buffer_rsrc_t rf =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.frags) + size_t(tile) * a.frag_stride, 0, int(a.frag_stride), BUF_DWORD3);
 #pragma unroll
@@ -568,7 +599,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
 #pragma unroll
     for (int c = 0; c < CPW; c++)
         if (c < nch) chunk_mfma<BITS, G16, S>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
-    if (do_rms) rms_finish(a, tile, W.cols, rms, inv);  // read after the barrier below
+    if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);  // read after the barrier below
 
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
     // rows 16 r + 4 (l / 16) + i of token l % 16.
@@ -672,20 +703,37 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
             }
         }
-        if constexpr (OUT_FLOW) qkv_signal(fl, rb, a.heads, a.kv_heads, a.hd);
+        if constexpr (OUT_FLOW) qkv_signal(fout, rb, a.heads, a.kv_heads, a.hd);
     } else if constexpr (EPI == EPI_RESID) {
-        for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
-            const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-            float xn = 0.0f;
-            if (tok < nt && row < W.rows) {
-                xn = __fadd_rn(xs[e], tl[e]);
-                a.out[size_t(ibase + tok) * a.ldo + row] = xn;
+        if constexpr (XCOH) {
+            // Residual rows, fragments and partials all go through the coherent path.
+            const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
+#pragma unroll
+            for (int u = 0; u < XR; u++) {
+                const int e = threadIdx.x + u * nthr, rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+                if (e >= rows_wg * FTOK) break;
+                float xn = 0.0f;
+                if (tok < nt && row < W.rows) {
+                    xn = __fadd_rn(xr[u], tl[e]);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xn), rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1);
+                }
+                tl[e] = xn;
             }
-            tl[e] = xn;
+        } else {
+            for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
+                const int rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+                float xn = 0.0f;
+                if (tok < nt && row < W.rows) {
+                    xn = __fadd_rn(xs[e], tl[e]);
+                    a.out[size_t(ibase + tok) * a.ldo + row] = xn;
+                }
+                tl[e] = xn;
+            }
         }
         __syncthreads();
         if (a.ofrags) {
             uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
+            const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(a.ofrag_stride), BUF_DWORD3);
             for (int q = threadIdx.x; q < (rows_wg / 8) * FTOK; q += nthr) {
                 const int cg = q / FTOK, tok = q % FTOK, col = row0 + 8 * cg;
                 float v[8];
@@ -694,16 +742,22 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                     const float x = tl[(8 * cg + j) * FTOK + tok];
                     v[j] = a.onorm ? __fmul_rn(x, vec[8 * cg + j]) : x;
                 }
-                write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
+                if constexpr (XCOH) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
+                else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
             }
         }
         if (a.oss) {
+            const __amdgpu_buffer_rsrc_t ros =
+                __builtin_amdgcn_make_buffer_rsrc(a.oss + size_t(tile) * a.oss_slots * FTOK, 0, a.oss_slots * FTOK * 4, BUF_DWORD3);
             for (int q = threadIdx.x; q < (rows_wg / 16) * FTOK; q += nthr) {
                 const int g = q / FTOK, tok = q % FTOK, slot = row0 / 16 + g;
                 if (slot >= a.oss_slots) continue;
-                a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] = ss16([&](int c) { return tl[(16 * g + c) * FTOK + tok]; }, 16);
+                const float v = ss16([&](int c) { return tl[(16 * g + c) * FTOK + tok]; }, 16);
+                if constexpr (XCOH) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ros, (slot * FTOK + tok) * 4, 0, CPOL_SC1);
+                else a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] = v;
             }
         }
+        if constexpr (XCOH) flow_signal(fout, rb);
     } else if constexpr (EPI == EPI_SILU) {
         // rows: [h gate rows | h up rows] for act columns h rb + [0, h), h = rows_wg / 2
         const int hw = rows_wg / 2;
@@ -727,7 +781,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             if constexpr (OUT_FLOW) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
             else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
-        if constexpr (OUT_FLOW) flow_signal(fl, rb);
+        if constexpr (OUT_FLOW) flow_signal(fout, rb);
     } else {
         // Output head: logits, optional store, per-token best (value, index) of this block.
         for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
@@ -794,7 +848,7 @@ __global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, 
     extern __shared__ __align__(16) uint8_t smem[];
     int bx = blockIdx.x, tile = blockIdx.y;
     if (gridDim.y > 1) xcd_tile_map(bx, tile);
-    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, bx, tile, smem);
+    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, Flow{}, bx, tile, smem);
 }
 
 // gate|up and down in one launch (one token tile): workgroups [0, n_gu) run gate|up and count
@@ -808,10 +862,10 @@ __global__ __launch_bounds__(1024) void k_gu_down(MMArgs gu, MMPlan pgu, MMArgs 
     const int ngu = pgu.nrb * pgu.nsplit;
     if (int(blockIdx.x) < ngu) {
         if (int(threadIdx.x) >= 64 * pgu.rg * pgu.kw) return;
-        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), false, true>(gu, pgu, sc, fl, blockIdx.x, 0, smem);
+        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), false, true>(gu, pgu, sc, Flow{}, fl, blockIdx.x, 0, smem);
     } else {
         if (int(threadIdx.x) >= 64 * pdn.rg * pdn.kw) return;
-        mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, false>(dn, pdn, sc, fl, blockIdx.x - ngu, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, false>(dn, pdn, sc, fl, Flow{}, blockIdx.x - ngu, 0, smem);
     }
 }
 
@@ -829,7 +883,7 @@ __global__ __launch_bounds__(512) void k_attn_o(AttnArgs aa, MMArgs o, MMPlan po
         attn_body<HD, true>(aa, int(blockIdx.x) % ASPLIT, int(blockIdx.x) / ASPLIT, 0, fl);
     } else {
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
-        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fl, int(blockIdx.x) - na, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fl, Flow{}, int(blockIdx.x) - na, 0, smem);
     }
 }
 
@@ -844,14 +898,132 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
     const int nq = pq.nrb * pq.nsplit, na = ASPLIT * aa.heads, bid = blockIdx.x;
     if (bid < nq) {
         if (int(threadIdx.x) >= 64 * pq.rg * pq.kw) return;
-        mm_body<BITS, EPI_QKV, G16, 1, false, true>(qa, pq, sc, fq, bid, 0, smem);
+        mm_body<BITS, EPI_QKV, G16, 1, false, true>(qa, pq, sc, Flow{}, fq, bid, 0, smem);
     } else if (bid < nq + na) {
         if (int(threadIdx.x) >= AWV * 64) return;
         attn_body<HD, true, true>(aa, (bid - nq) % ASPLIT, (bid - nq) / ASPLIT, 0, fo, fq);
     } else {
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
-        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fo, bid - nq - na, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fo, Flow{}, bid - nq - na, 0, smem);
     }
+}
+
+// Every layer of a one-tile pass in one launch. The workgroups of layer l follow those of layer
+// l - 1, and inside a layer come q|k|v (one per strip), attention (ASPLIT per head), o, gate|up
+// and down (K splits of a row block side by side), so every workgroup waits only for workgroups
+// with lower indices. Those are dispatched before it: whatever the number of workgroups resident
+// at once, the lowest unfinished one always has its inputs, and the launch cannot deadlock.
+// Workgroups of later stages and layers are dispatched while earlier ones still wait or work,
+// issue their weight loads at once, and only then wait for their input. Counters (per layer,
+// FLOW_LAYER_STRIDE apart): q|k|v -> attention one per head, attention -> o, o -> gate|up,
+// gate|up -> down one per down K split, down -> the next layer's q|k|v.
+template <int HD, int BITS, bool G16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
+                                                MMArgs oa, MMPlan po, MMArgs ga, MMPlan pg, MMArgs da, MMPlan pd, MMScratch sc,
+                                                LayerFlows lf) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int nq = pq.nrb, na = ASPLIT * aa.heads, no = po.nrb, ng = pg.nrb, nd = pd.nrb * pd.nsplit;
+    const int per_layer = nq + na + no + ng + nd;
+    const int l = int(blockIdx.x) / per_layer;
+    int r = int(blockIdx.x) % per_layer;
+    const LayerPtrs& P = lp[l];
+    const int base = FLOW_COUNTERS + FLOW_LAYER_STRIDE * l;
+    const bool last = l + 1 == lf.layers;
+    if (r < nq) {
+        if (int(threadIdx.x) >= 64 * pq.kw) return;
+        MMArgs a = qa;
+        a.W = P.qkv;
+        a.bias = P.b_qkv;
+        a.kcache = P.kc + seq_off;
+        a.vcache = P.vc + seq_off;
+        Flow fin;  // the previous layer's down row blocks (layer 0: written before the launch)
+        if (l > 0) {
+            fin.ctl = lf.ctl;
+            fin.producers = fin.per = pd.nrb;
+            fin.consumers = nq;
+            fin.base = base - FLOW_LAYER_STRIDE + FL_D;
+            fin.mirrors = lf.m_d;
+        }
+        Flow fout;
+        fout.ctl = lf.ctl;
+        fout.producers = nq;
+        fout.want = 3 * (HD / 16);
+        fout.consumers = ASPLIT;
+        fout.base = base + FL_Q;
+        mm_body<BITS, EPI_QKV, G16, 1, true, true>(a, pq, sc, fin, fout, r, 0, smem);
+        return;
+    }
+    r -= nq;
+    if (r < na) {
+        if (int(threadIdx.x) >= AWV * 64) return;
+        AttnArgs A = aa;
+        A.kc = P.kc + seq_off;
+        A.vc = P.vc + seq_off;
+        Flow fin;
+        fin.ctl = lf.ctl;
+        fin.producers = nq;
+        fin.want = 3 * (HD / 16);
+        fin.consumers = ASPLIT;
+        fin.base = base + FL_Q;
+        Flow fout;
+        fout.ctl = lf.ctl;
+        fout.producers = fout.per = aa.heads;
+        fout.consumers = no;
+        fout.base = base + FL_A;
+        fout.mirrors = lf.m_a;
+        attn_body<HD, true, true>(A, r % ASPLIT, r / ASPLIT, 0, fout, fin);
+        return;
+    }
+    r -= na;
+    Flow fo;  // o -> gate|up
+    fo.ctl = lf.ctl;
+    fo.producers = fo.per = no;
+    fo.consumers = ng;
+    fo.base = base + FL_O;
+    fo.mirrors = lf.m_o;
+    Flow fg;  // gate|up -> down, one counter per down K split
+    fg.ctl = lf.ctl;
+    fg.producers = ng;
+    fg.per = lf.gu_per;
+    fg.consumers = pd.nrb;
+    fg.base = base + FL_G;
+    fg.mirrors = lf.m_g;
+    if (r < no) {
+        if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
+        MMArgs a = oa;
+        a.W = P.o;
+        a.onorm = P.post_norm;
+        Flow fin;
+        fin.ctl = lf.ctl;
+        fin.producers = fin.per = aa.heads;
+        fin.consumers = no;
+        fin.base = base + FL_A;
+        fin.mirrors = lf.m_a;
+        mm_body<BITS, EPI_RESID, G16, 1, true, true>(a, po, sc, fin, fo, r, 0, smem);
+        return;
+    }
+    r -= no;
+    if (r < ng) {
+        if (int(threadIdx.x) >= 64 * pg.rg * pg.kw) return;
+        MMArgs a = ga;
+        a.W = P.gu;
+        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true>(a, pg, sc, fo, fg, r, 0, smem);
+        return;
+    }
+    r -= ng;
+    if (int(threadIdx.x) >= 64 * pd.rg * pd.kw) return;
+    MMArgs a = da;
+    a.W = P.down;
+    a.onorm = P.next_norm;
+    Flow fout;  // the next layer's q|k|v; after the last layer the head reads x in a later launch
+    if (!last) {
+        fout.ctl = lf.ctl;
+        fout.producers = fout.per = pd.nrb;
+        fout.consumers = nq;
+        fout.base = base + FL_D;
+        fout.mirrors = lf.m_d;
+    }
+    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true>(a, pd, sc, fg, fout, r, 0, smem);
 }
 
 // Output head, persistent: each workgroup copies the tile's fragments (every k-step) to LDS
@@ -1117,7 +1289,8 @@ void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, cons
     fl.producers = pgu.nrb;
     fl.per = split_cols / act_cols;
     fl.consumers = pdn.nrb;
-    if (split_cols % act_cols || (fl.producers + fl.per - 1) / fl.per != pdn.nsplit || pdn.nsplit > FLOW_COUNTERS)
+    fl.mirrors = std::min(FLOW_GU_MIRRORS, pdn.nrb);
+    if (split_cols % act_cols || (fl.producers + fl.per - 1) / fl.per != pdn.nsplit || pdn.nsplit * fl.mirrors > FLOW_ATTN_O)
         throw std::runtime_error("gate|up row blocks do not map onto the down K splits");
     const int n = pgu.nrb * pgu.nsplit + pdn.nrb * pdn.nsplit;
     const size_t lds = std::max(lds_bytes(pgu), lds_bytes(pdn));
@@ -1171,6 +1344,7 @@ void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd
     fl.per = heads;
     fl.consumers = po.nrb * po.nsplit;
     fl.base = FLOW_ATTN_O;
+    fl.mirrors = std::min(FLOW_AO_MIRRORS, fl.consumers);
     switch (hd) {
         case 16: launch_attn_o<16>(aa, o, po, sc, fl, s); break;
         case 32: launch_attn_o<32>(aa, o, po, sc, fl, s); break;
@@ -1207,7 +1381,7 @@ static void launch_qkv_attn_o(const MMArgs& qa, const MMPlan& pq, const AttnArgs
 void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cnt, uint8_t* frags, const MMArgs& o, const MMPlan& po,
                      const MMScratch& sc, int* ctl, hipStream_t s) {
     const int heads = qa.heads, kvh = qa.kv_heads, hd = qa.hd, t = qa.n;
-    if (t > FTOK || pq.tiles != 1 || po.tiles != 1) throw std::runtime_error("the fused q|k|v/attention/o launch takes one token tile");
+    if (t < 1 || t > FTOK || pq.tiles != 1 || po.tiles != 1) throw std::runtime_error("the fused q|k|v/attention/o launch takes one token tile");
     if (pq.s != 1 || pq.rg != 1 || pq.nsplit != 1) throw std::runtime_error("the fused launch needs q|k|v as one workgroup per strip");
     if (po.s != 1 || po.nsplit != 1) throw std::runtime_error("the fused launch needs o without a K split");
     if (64 * po.rg * po.kw > 512 || 64 * pq.kw > 512) throw std::runtime_error("workgroups too large for the fused launch");
@@ -1228,12 +1402,82 @@ void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cn
     fo.per = heads;
     fo.consumers = po.nrb * po.nsplit;
     fo.base = FLOW_ATTN_O;
+    fo.mirrors = std::min(FLOW_AO_MIRRORS, fo.consumers);
     switch (hd) {
         case 16: launch_qkv_attn_o<16>(qa, pq, aa, o, po, sc, fq, fo, s); break;
         case 32: launch_qkv_attn_o<32>(qa, pq, aa, o, po, sc, fq, fo, s); break;
         case 64: launch_qkv_attn_o<64>(qa, pq, aa, o, po, sc, fq, fo, s); break;
         case 128: launch_qkv_attn_o<128>(qa, pq, aa, o, po, sc, fq, fo, s); break;
         default: throw std::runtime_error("head_dim must be 16, 32, 64 or 128");
+    }
+}
+
+int layer_stack_workgroups(int heads, const MMPlan& pq, const MMPlan& po, const MMPlan& pg, const MMPlan& pd) {
+    return pq.nrb + ASPLIT * heads + po.nrb + pg.nrb + pd.nrb * pd.nsplit;
+}
+
+const char* layer_stack_unfit(int t, int heads, int kv_heads, int hd, const MMPlan& pq, const MMPlan& po, const MMPlan& pg,
+                              const MMPlan& pd) {
+    if (t < 1 || t > FTOK || pq.tiles != 1 || po.tiles != 1 || pg.tiles != 1 || pd.tiles != 1) return "the layer stack takes one token tile";
+    if (pq.s != 1 || pq.rg != 1 || pq.nsplit != 1) return "the layer stack needs q|k|v as one workgroup per strip";
+    if (po.s != 1 || po.nsplit != 1) return "the layer stack needs o without a K split";
+    if (pg.nsplit != 1 || pg.s * pg.rg != 2 * GU_STRIPS) return "the layer stack needs gate|up row blocks without a K split";
+    if (pd.s != DOWN_STRIPS) return "the layer stack needs the down plan's strips per wavefront";
+    if (pd.nsplit * FLOW_GU_MIRRORS > FLOW_LAYER_STRIDE - FL_G) return "too many down K splits for the layer counters";
+    const int split_cols = 128 * pd.kw, act_cols = 16 * GU_STRIPS;
+    if (split_cols % act_cols || (pg.nrb + split_cols / act_cols - 1) / (split_cols / act_cols) != pd.nsplit)
+        return "gate|up row blocks do not map onto the down K splits";
+    if (std::max({64 * pq.kw, AWV * 64, 64 * po.rg * po.kw, 64 * pg.rg * pg.kw, 64 * pd.rg * pd.kw}) > 512)
+        return "workgroups too large for the layer stack";
+    if (po.s > po.kw || pd.s > pd.kw) return "residual rows do not fit the per-thread registers";
+    if (heads > FL_A - FL_Q || hd % 16 || heads % kv_heads) return "heads do not fit the layer counters";
+    if (hd != 16 && hd != 32 && hd != 64 && hd != 128) return "head_dim must be 16, 32, 64 or 128";
+    if (hd / 2 > ROPE_HALF_MAX || (heads + kv_heads) * hd % 16) return "head_dim must be even and at most 256";
+    return nullptr;
+}
+
+template <int HD>
+static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& qa, const MMPlan& pq, const AttnArgs& aa,
+                          const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da, const MMPlan& pd,
+                          const MMScratch& sc, const LayerFlows& lf, hipStream_t s) {
+    const dim3 grid(layers * layer_stack_workgroups(aa.heads, pq, po, pg, pd)), block(512);
+    const size_t lds = std::max({lds_bytes(pq), lds_bytes(po), lds_bytes(pg), lds_bytes(pd)});
+    const bool g16 = qa.W.bits != 16 && qa.W.group == 16;
+    switch (qa.W.bits) {
+        case 16: go(k_layers<HD, 16, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+        case 8:
+            if (g16) go(k_layers<HD, 8, true>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+            else go(k_layers<HD, 8, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+            break;
+        default:
+            if (g16) go(k_layers<HD, 4, true>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+            else go(k_layers<HD, 4, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+            break;
+    }
+    FCHECK(hipGetLastError());
+}
+
+void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& qa, const MMPlan& pq, float* attn_scratch, int* attn_cnt,
+                 uint8_t* af, const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da,
+                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s) {
+    const int heads = qa.heads, kvh = qa.kv_heads, hd = qa.hd, t = qa.n;
+    if (const char* why = layer_stack_unfit(t, heads, kvh, hd, pq, po, pg, pd)) throw std::runtime_error(why);
+    if (pd.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
+    if (layers < 1) throw std::runtime_error("the layer stack needs at least one layer");
+    const AttnArgs aa = make_attn_args(qa.out, qa.ldo, t, heads, kvh, hd, qa.pos0, AttnRows{}, nullptr, nullptr, attn_scratch, attn_cnt, af);
+    LayerFlows lf;
+    lf.ctl = ctl;
+    lf.layers = layers;
+    lf.gu_per = 128 * pd.kw / (16 * GU_STRIPS);
+    lf.m_a = std::min<int>(FL_MIRRORS, po.nrb);
+    lf.m_o = std::min<int>(FL_MIRRORS, pg.nrb);
+    lf.m_d = std::min<int>(FL_MIRRORS, pq.nrb);
+    lf.m_g = std::min<int>(FLOW_GU_MIRRORS, pd.nrb);
+    switch (hd) {
+        case 16: launch_layers<16>(lp, layers, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf, s); break;
+        case 32: launch_layers<32>(lp, layers, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf, s); break;
+        case 64: launch_layers<64>(lp, layers, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf, s); break;
+        default: launch_layers<128>(lp, layers, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf, s); break;
     }
 }
 

@@ -148,18 +148,27 @@ struct MMScratch {
 // reaches the number of producers that feed it, count themselves in the counter's second word,
 // and the last of `consumers` puts both words back to zero. Counters sit FLOW_CNT_STRIDE words
 // apart (their own cache lines). A wait that gives up sets the error word and goes on.
+//
+// A counter with many consumers is mirrored: each producer adds 1 to `mirrors` copies on
+// separate lines and consumer w polls copy w % mirrors, so that no line is polled by more than
+// a few workgroups (atomics on one line are served one after another). Counter j, copy m is
+// slot base + j mirrors + m; the consumer count sits beside copy 0. Every copy must have a
+// consumer (mirrors <= consumers, consumers numbered 0, 1, ...), so that every copy is complete
+// before the last consumer resets them.
 struct Flow {
     int* ctl = nullptr;  // control block, FLOW_WORDS ints, zero between launches
     int producers = 0;
     int per = 1;        // producers per counter
     int consumers = 0;  // consumer workgroups per counter
-    int base = 0;       // first counter of this launch
+    int base = 0;       // first counter slot of this launch
     int want = 0;       // when set: the count every counter waits for (producers may feed several)
+    int mirrors = 1;    // copies of each counter
 };
-// Control block words: error flag, greedy acceptance (m, next), then the counters (gate|up ->
-// down from counter 0; q|k|v -> attention one per head from counter 0; attention -> o at
-// FLOW_ATTN_O).
-enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 32, FLOW_ATTN_O = FLOW_COUNTERS - 1 };
+// Control block words: error flag, greedy acceptance (m, next), then the counter slots (gate|up
+// -> down from slot 0, FLOW_GU_MIRRORS per down K split; q|k|v -> attention one per head from
+// slot 0; attention -> o at FLOW_ATTN_O, FLOW_AO_MIRRORS copies).
+enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 48, FLOW_ATTN_O = 40 };
+constexpr int FLOW_GU_MIRRORS = 2, FLOW_AO_MIRRORS = 8;
 constexpr int FLOW_WORDS = FLOW_CNT0 + FLOW_CNT_STRIDE * FLOW_COUNTERS;
 
 // QKV projection + 1/rms + bias + RoPE + K/V append (plan strips 1). Rows: q heads and k heads
@@ -195,6 +204,45 @@ void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cn
                      const MMScratch& sc, int* ctl, hipStream_t s);
 // Workgroups of a qkv_attention_o launch.
 int qkv_attention_o_workgroups(int heads, const MMPlan& pq, const MMPlan& po);
+
+// Weights, vectors and caches of one resident layer, for the layer-stack launch (a device array,
+// one entry per layer).
+struct LayerPtrs {
+    TMat qkv, o, gu, down;
+    const float* b_qkv = nullptr;
+    const float* post_norm = nullptr;
+    const float* next_norm = nullptr;  // the next layer's input norm; the final norm after the last layer
+    float* kc = nullptr;               // this layer's K/V cache rows of sequence 0
+    float* vc = nullptr;
+};
+// Counter slots of the layer-stack launch: FLOW_LAYER_STRIDE per layer after the FLOW_COUNTERS of
+// the per-layer launches. Inside a layer's block: q|k|v -> attention from FL_Q (one per head),
+// attention -> o at FL_A, o -> gate|up at FL_O, down -> the next layer's q|k|v at FL_D (each
+// FL_MIRRORS copies), gate|up -> down from FL_G (FLOW_GU_MIRRORS copies per down K split).
+enum { FLOW_LAYER_STRIDE = 160, FL_Q = 0, FL_A = 32, FL_O = 48, FL_D = 64, FL_G = 80, FL_MIRRORS = 16 };
+// Words of a control block that serves launches over `layers` layers.
+inline size_t flow_words(int layers) {
+    return FLOW_CNT0 + size_t(FLOW_CNT_STRIDE) * (FLOW_COUNTERS + size_t(FLOW_LAYER_STRIDE) * size_t(layers));
+}
+struct LayerFlows {
+    int* ctl = nullptr;
+    int layers = 0;
+    int gu_per = 1;                      // gate|up row blocks per down K split
+    int m_a = 1, m_o = 1, m_d = 1, m_g = 1;  // copies of the attention -> o, o -> gate|up, down -> q|k|v, gate|up -> down counters
+};
+// Workgroups of one layer in the layer-stack launch.
+int layer_stack_workgroups(int heads, const MMPlan& pq, const MMPlan& po, const MMPlan& pg, const MMPlan& pd);
+// Why plans of a pass over t tokens cannot run as a layer stack, or null when they can.
+const char* layer_stack_unfit(int t, int heads, int kv_heads, int hd, const MMPlan& pq, const MMPlan& po, const MMPlan& pg,
+                              const MMPlan& pd);
+// Every layer of a one-tile pass in one launch: per layer q|k|v (+ RoPE, K/V append), attention,
+// o (+ residual), gate|up (+ SiLU) and down (+ residual), the same plans and so the same bits as
+// the per-layer launches. qa/oa/ga/da carry everything but the per-layer pointers, which come
+// from lp (caches offset by seq_off floats). The fragments and partials of x * next_norm after
+// the last layer are left for the head. ctl holds flow_words(layers) words, zero between launches.
+void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& qa, const MMPlan& pq, float* attn_scratch, int* attn_cnt,
+                 uint8_t* af, const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da,
+                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s);
 
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
 // partials at [tile][arg_off + b][16] for b below the returned count.

@@ -493,6 +493,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
     if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
+    if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default off)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -533,13 +534,33 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     // Staging (ints): a call's chunk positions and tokens, or a batch's segments, rows and blocks.
     const size_t stage_words = std::max(max_ctx / PREFILL_CHUNK + 2 + max_ctx, 4 * max_segs + 3 * T + 2 * size_t(n_seq));
     stage_ = DevBuf(stage_words * 4);
-    ctl_ = DevBuf(FLOW_WORDS * 4);
+    ctl_ = DevBuf(flow_words(int(c.layers)) * 4);
     HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
     bacc_ = DevBuf((1 + 2 * size_t(n_seq)) * 4);
     h_stage_ = PinnedBuf(stage_words * 4);
     h_out_ = PinnedBuf(PREFILL_CHUNK * 4);
     h_ctl_ = PinnedBuf(CTL_BACK * 4);
     h_bacc_ = PinnedBuf((1 + 2 * size_t(n_seq)) * 4);
+    if (prov_->resident()) {
+        // Layer pointers for the layer-stack launch; caches of sequence 0 (a selected sequence
+        // adds its offset at launch).
+        std::vector<LayerPtrs> lp(c.layers);
+        for (size_t l = 0; l < c.layers; l++) {
+            const DevLayer& L = prov_->layer(l);
+            LayerPtrs& P = lp[l];
+            P.qkv = L.qkv;
+            P.o = L.o;
+            P.gu = L.gu;
+            P.down = L.down;
+            P.b_qkv = L.b_qkv;
+            P.post_norm = L.post_norm;
+            P.next_norm = l + 1 < c.layers ? prov_->layer(l + 1).in_norm : fnorm_.as<float>();
+            P.kc = kcache_.as<float>() + l * size_t(n_seq) * max_ctx * kv;
+            P.vc = vcache_.as<float>() + l * size_t(n_seq) * max_ctx * kv;
+        }
+        layer_ptrs_ = DevBuf(lp.size() * sizeof(LayerPtrs));
+        HIPC(hipMemcpyAsync(layer_ptrs_.p, lp.data(), layer_ptrs_.n, hipMemcpyHostToDevice, stream_));
+    }
     HIPC(hipStreamSynchronize(stream_));
 }
 
@@ -678,7 +699,76 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     // arrived.
     const DevLayer* L0 = res ? &prov_->layer(0) : nullptr;
     prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr);
-    for (size_t l = 0; l < c.layers; l++) {
+    bool stacked = false;
+    if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
+        // One launch for every layer: the same plans (so the same bits) as the per-layer
+        // launches below.
+        const MMPlan pq = mm_plan(L0->qkv, 1, kw_qkv_, T, 1), po = mm_plan(L0->o, 1, kw_o_, T, 1);
+        const MMPlan pg = gu_plan(L0->gu, kw_gu_, T), pd = mm_plan(L0->down, 1, kw_down_, T, DOWN_STRIPS);
+        if (!layer_stack_unfit(T, heads, kvh, hd, pq, po, pg, pd)) {
+            MMArgs qa;
+            qa.W = L0->qkv;
+            qa.frags = xf;
+            qa.frag_stride = fb_h_;
+            qa.ss = ss;
+            qa.ss_slots = slots_h_;
+            qa.eps = c.eps;
+            qa.n = T;
+            qa.out = q_.as<float>();
+            qa.ldo = hq;
+            qa.rope_cos = rope_cos_.as<float>();
+            qa.rope_sin = rope_sin_.as<float>();
+            qa.pos0 = pos_dev;
+            qa.heads = heads;
+            qa.kv_heads = kvh;
+            qa.hd = hd;
+            MMArgs oa;
+            oa.W = L0->o;
+            oa.frags = af_.as<uint8_t>();
+            oa.frag_stride = fb_q_;
+            oa.n = T;
+            oa.out = x;
+            oa.ldo = h;
+            oa.ofrags = xf;
+            oa.ofrag_stride = fb_h_;
+            oa.oss = ss;
+            oa.oss_slots = slots_h_;
+            MMArgs ga;
+            ga.W = L0->gu;
+            ga.frags = xf;
+            ga.frag_stride = fb_h_;
+            ga.ss = ss;
+            ga.ss_slots = slots_h_;
+            ga.eps = c.eps;
+            ga.n = T;
+            ga.ofrags = actf_.as<uint8_t>();
+            ga.ofrag_stride = fb_in_;
+            MMArgs da;
+            da.W = L0->down;
+            da.frags = actf_.as<uint8_t>();
+            da.frag_stride = fb_in_;
+            da.n = T;
+            da.out = x;
+            da.ldo = h;
+            da.ofrags = xf;
+            da.ofrag_stride = fb_h_;
+            da.oss = ss;
+            da.oss_slots = slots_h_;
+            prof_begin();
+            layer_stack(layer_ptrs_.as<LayerPtrs>(), int(c.layers), size_t(cur_) * max_ctx_ * kv, qa, pq, attn_scratch_.as<float>(),
+                        attn_cnt_.as<int>(), af_.as<uint8_t>(), oa, po, ga, pg, da, pd, scr, ctl_.as<int>(), s);
+            for (size_t l = 0; l < c.layers; l++) {
+                const DevLayer& L = prov_->layer(l);
+                prof_end(L.qkv, T, l == 0);
+                prof_end(L.o, T, false, 2.0 * kv * 4 * double(pos_ + T));  // + the K/V rows attention reads
+                prof_end(L.gu, T, false);
+                prof_end(L.down, T, false);
+                prov_->release_layer(l);
+            }
+            stacked = true;
+        }
+    }
+    for (size_t l = 0; !stacked && l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
         // This layer's caches: every sequence's for a batch, else the selected one's.
         const size_t cache_off = (l * size_t(n_seq_) + (bv ? 0 : size_t(cur_))) * max_ctx_ * kv;
@@ -916,7 +1006,7 @@ void Model::verify_body(const uint32_t* block, size_t n) {
 // leaves garbage behind: report it and clear the control block for the next call.
 void Model::check_flow(const int* ctl) {
     if (ctl[FLOW_ERR] == 0) return;
-    HIPC(hipMemsetAsync(ctl_.p, 0, FLOW_WORDS * 4, stream_));
+    HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
     HIPC(hipStreamSynchronize(stream_));
     fail("a fused launch timed out waiting for its producers; the results of this call are invalid", LS_E_DEVICE);
 }

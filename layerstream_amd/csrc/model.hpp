@@ -172,18 +172,21 @@ private:
     // input; af_: attention output fragments; actf_: SiLU(g) * u fragments; part_/cnt_: split-K
     // scratch; hpv_/hpi_: head-block argmax partials; row0_: logits of row 0.
     DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, ctl_, bacc_;
+    // Resident models: every layer's pointers for the layer-stack launch (LayerPtrs per layer).
+    DevBuf layer_ptrs_;
     PinnedBuf h_stage_, h_out_, h_ctl_, h_bacc_;
     // Control block: FLOW_WORDS words of fused-launch counters, then the acceptance (m, next).
     static constexpr int CTL_BACK = FLOW_ACC + 2;  // control words copied back after a pass: error, acceptance
     bool fuse_on_ = true;
     bool fuse_qkv_ = true;  // q|k|v joins the attention + o launch
     bool pf_on_ = true;     // fused consumers prefetch the next launch's weights
+    bool stack_on_ = false;  // one-tile passes over resident layers run as one layer-stack launch (LS_STACK=1)
     const int* stage_pos_ = nullptr;  // device positions of the staged chunks
     size_t vpad_ = 0, fb_h_ = 0, fb_q_ = 0, fb_in_ = 0;
     int head_blocks_ = 0, slots_h_ = 0;
     size_t head_off_ = 0;  // launch row of the first requested head row
     // wavefronts along K per row group: q|k|v, o, gate|up, down, head
-    int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 13, kw_head_ = 7;
+    int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 8, kw_head_ = 7;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     bool prof_ = false;
