@@ -87,12 +87,7 @@ __device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
         int zero = 0;
         asm volatile("" : "+v"(zero));
         unsigned spins = 0;
-#ifdef LS_POLL_LOAD
-        const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(cnt, 0, 4, BUF_DWORD3);
-        while (int(__builtin_amdgcn_raw_buffer_load_b32(rc, 0, 0, CPOL_SC1)) < want) {
-#else
         while (__hip_atomic_fetch_add(cnt, zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want) {
-#endif
             if (++spins > FLOW_SPIN_LIMIT) {
                 __hip_atomic_store(fl.ctl + FLOW_ERR, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
