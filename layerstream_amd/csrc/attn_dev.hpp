@@ -18,14 +18,14 @@ namespace ls {
 // (q . k_j) * scale, a softmax (max, exp(x - max), sum, * 1/sum) and sum_j p_j v_j over every
 // cached position.
 //
-// One launch: grid (ASPLIT, heads, row segments) of 4-wavefront workgroups. A segment is a run
+// One launch: grid (ASPLIT, heads, row segments) of AWV-wavefront workgroups. A segment is a run
 // of at most 16 consecutive rows of one sequence inside one 16-row tile: every token tile of a
 // single sequence, or the pieces of a batch of sequences cut at tile boundaries. The keys are
-// cut into 16-key blocks; block b belongs to wavefront b % (4 ASPLIT) of the (head, segment)
-// (workgroup (b % (4 ASPLIT)) / 4), which keeps a running (max, sum, output) per token over its
+// cut into 16-key blocks; block b belongs to wavefront b % (AWV ASPLIT) of the (head, segment)
+// (workgroup (b % (AWV ASPLIT)) / AWV), which keeps a running (max, sum, output) per token over its
 // blocks in order (online softmax) without any barrier: the scores ([keys][tokens]) and the
 // weighted sum ([dims][tokens]) run on v_mfma_f32_16x16x4f32 straight from registers, each lane
-// loading the K, V and q values it feeds (the next block's while this one computes). The four
+// loading the K, V and q values it feeds (the next block's while this one computes). The AWV
 // wavefronts' states merge in LDS in wavefront order, and the last of the ASPLIT workgroups to
 // finish (an agent-scope counter) merges theirs in workgroup order and writes the output rows as
 // fragments. Which blocks a wavefront takes depends only on key positions, so a token's result
@@ -34,7 +34,7 @@ namespace ls {
 // ---------------------------------------------------------------------------------------
 constexpr int AKB = 16;    // keys per block
 constexpr int ATQ = 16;    // query tokens per tile
-constexpr int AWV = 4;     // wavefronts per workgroup
+constexpr int AWV = 8;     // wavefronts per workgroup
 constexpr int ASPLIT = ATTN_SPLIT;
 typedef float attn_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t attn_u32x4 __attribute__((ext_vector_type(4)));
@@ -309,7 +309,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         block(b + stride, bb);
     }
 
-    // The four wavefronts' states, merged in wavefront order into this workgroup's state.
+    // The AWV wavefronts' states, merged in wavefront order into this workgroup's state.
     float L = Lp + __shfl_xor(Lp, 16, 64);
     L += __shfl_xor(L, 32, 64);
     if (g == 0) {
@@ -412,7 +412,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     __syncthreads();
     uint8_t* tf = frags + size_t(tile) * frag_stride;
     const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(frag_stride), BUF_DWORD3);
-    for (int p = tid; p < nq * (HD / 8); p += 256) {
+    for (int p = tid; p < nq * (HD / 8); p += AWV * 64) {
         const int i = p / (HD / 8), sl = p % (HD / 8), col = head * HD + 8 * sl;
         if constexpr (OUT_FLOW) write_slot_coherent(rf, 0, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
         else write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);

@@ -23,7 +23,7 @@ namespace ls {
     } while (0)
 
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(AWV * 64) void k_attn(AttnArgs a) {
     attn_body<HD, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, Flow{});
 }
 
