@@ -844,7 +844,7 @@ __device__ __forceinline__ void xcd_tile_map(int& bx, int& tile) {
 }
 
 template <int BITS, int EPI, bool G16, int S>
-__global__ __launch_bounds__(S == 4 ? 512 : 1024) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+__global__ __launch_bounds__(mm_max_waves(BITS, G16 ? 16 : 32, S) * 64) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     extern __shared__ __align__(16) uint8_t smem[];
     int bx = blockIdx.x, tile = blockIdx.y;
     if (gridDim.y > 1) xcd_tile_map(bx, tile);
@@ -918,7 +918,7 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
 // FLOW_LAYER_STRIDE apart): q|k|v -> attention one per head, attention -> o, o -> gate|up,
 // gate|up -> down one per down K split, down -> the next layer's q|k|v.
 template <int HD, int BITS, bool G16>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
+__global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
                                                 MMArgs oa, MMPlan po, MMArgs ga, MMPlan pg, MMArgs da, MMPlan pd, MMScratch sc,
                                                 LayerFlows lf) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1182,7 +1182,7 @@ MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
     p.s = strips;
     p.rg = rg;
     p.kw = kw < 1 ? 1 : kw;
-    const int max_waves = strips == 4 ? 8 : 16;
+    const int max_waves = mm_max_waves(W.bits, W.group, strips);
     const int cpw = 4 / (W.bits == 16 ? 1 : (W.bits == 8 ? 2 : 4));
     const int waves_k = (W.n_chunks + cpw - 1) / cpw;  // wavefront shares along K
     if (p.kw > waves_k) p.kw = waves_k;

@@ -126,6 +126,12 @@ struct MMArgs {
 struct MMPlan {
     int s = 1, rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
 };
+// Wavefronts a matrix workgroup may hold: 16 (1024 threads, at most 128 registers each), but 8
+// for four bf16 or groups-of-16 strips per wavefront, whose wider chunks or extra MFMAs need more
+// registers.
+__host__ __device__ constexpr int mm_max_waves(int bits, int group, int strips) {
+    return (strips == 4 && (bits == 16 || group == 16)) ? 8 : 16;
+}
 MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips);
 // The gate|up plan: gu_wave_strips strips per wavefront, row groups making one gate and up block.
 MMPlan gu_plan(const TMat& W, int kw, int n_tokens);

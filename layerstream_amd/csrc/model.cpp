@@ -489,6 +489,8 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const size_t n_chunks = (c.vocab + STREAM_HEAD_ROWS - 1) / STREAM_HEAD_ROWS;
         head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * STREAM_HEAD_ROWS / 64));
     }
+    // Wide rows (3B: 32 int8 chunks) fill a 16-wavefront workgroup along K with no split.
+    if (c.hidden >= 2048) kw_qkv_ = kw_o_ = kw_gu_ = kw_down_ = kw_head_ = 16;
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
