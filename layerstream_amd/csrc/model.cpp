@@ -495,7 +495,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
     if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
-    if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default off)
+    if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default on)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
