@@ -198,6 +198,67 @@ def roofline_of(prof, kernel, traffic_path):
     }
 
 
+def _csv_rows(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _col(row, *names):
+    for n in names:
+        if n in row:
+            return n
+    raise KeyError(f"none of {names} in the CSV columns {sorted(row)}")
+
+
+def _short(name):
+    return name.split("(")[0].replace("void ", "").strip()
+
+
+def summarize(args):
+    """Per-kernel figures over the last --last verify steps of a profiled bench run (each step
+    ends with k_head_final): durations from a --kernel-trace CSV, or counters from a --pmc CSV."""
+    if args.trace_summary:
+        rows = _csv_rows(args.trace_summary)
+        kn, ts, te = _col(rows[0], "Kernel_Name"), _col(rows[0], "Start_Timestamp"), _col(rows[0], "End_Timestamp")
+        rows.sort(key=lambda r: int(r[ts]))
+        ends = [i for i, r in enumerate(rows) if "k_head_final" in r[kn]]
+        if len(ends) <= args.last:
+            raise SystemExit(f"the trace holds {len(ends)} verify steps, fewer than --last {args.last} + 1")
+        sel = rows[ends[-args.last - 1] + 1 : ends[-1] + 1]
+        stats = {}
+        for r in sel:
+            stats.setdefault(_short(r[kn]), []).append((int(r[te]) - int(r[ts])) / 1e3)
+        print(f"| kernel | launches / step | avg us | min us | max us | us / step |\n|---|---|---|---|---|---|")
+        for k, v in sorted(stats.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| `{k}` | {len(v) / args.last:g} | {np.mean(v):.2f} | {np.min(v):.2f} | {np.max(v):.2f} | {sum(v) / args.last:.1f} |")
+        busy = sum(sum(v) for v in stats.values()) / args.last
+        print(f"\nBusy time per step: {busy:.1f} us over the last {args.last} verify steps.")
+    if args.pmc_summary:
+        rows = _csv_rows(args.pmc_summary)
+        kn, cn, cv = _col(rows[0], "Kernel_Name"), _col(rows[0], "Counter_Name"), _col(rows[0], "Counter_Value")
+        di = _col(rows[0], "Dispatch_Id", "Correlation_Id")
+        disp = {}
+        for r in rows:
+            d = disp.setdefault(int(r[di]), {"name": _short(r[kn])})
+            d[r[cn]] = d.get(r[cn], 0.0) + float(r[cv])
+        order = sorted(disp)
+        ends = [d for d in order if "k_head_final" in disp[d]["name"]]
+        if len(ends) <= args.last:
+            raise SystemExit(f"the counters cover {len(ends)} verify steps, fewer than --last {args.last} + 1")
+        sel = [disp[d] for d in order if ends[-args.last - 1] < d <= ends[-1]]
+        names = sorted({k for d in sel for k in d if k != "name"})
+        stats = {}
+        for d in sel:
+            stats.setdefault(d["name"], []).append(d)
+        print("| kernel | launches / step | " + " | ".join(f"{n} KiB / launch" for n in names) + " |")
+        print("|---|---|" + "---|" * len(names))
+        for k, v in sorted(stats.items(), key=lambda kv: -sum(x.get(names[0], 0) for x in kv[1])):
+            vals = " | ".join(f"{np.mean([x.get(n, 0.0) for x in v]):.1f}" for n in names)
+            print(f"| `{k}` | {len(v) / args.last:g} | {vals} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -213,7 +274,13 @@ def main():
     ap.add_argument("--no-graphs", action="store_true", help="launch each kernel of a verify step separately (for tracers)")
     ap.add_argument("--greedy-ref", type=int, default=GREEDY_REF, help="tokens of greedy continuation scripting the drafter")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    ap.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel-trace CSV of a bench run and exit")
+    ap.add_argument("--pmc-summary", metavar="CSV", help="summarise a rocprofv3 counter-collection CSV of a bench run and exit")
+    ap.add_argument("--last", type=int, default=ROOF_STEPS, help="verify steps the summaries cover (the last ones of the run)")
     args = ap.parse_args()
+    if args.trace_summary or args.pmc_summary:
+        summarize(args)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -313,9 +380,15 @@ def run_single(args, conf):
     sb = step_bytes(cfg, layer_bytes, row_bytes, ctx_mean, k + 1)
     step_ms_p50 = float(np.median(tms))
     tag = model_tag(conf)
-    traffic_path = os.path.join(ROOT, "profiles", f"k_mm_{tag}_verify_hbm_traffic.md")
-    roofline = roofline_of(prof, f"matrix launches (MFMA weight streaming): k_mm q|k|v and o, k_gu_down gate|up + down, k_head; "
-                           f"{FMT_NAME[conf['fmt'][0]]}, t={k + 1}", traffic_path)
+    per_step = prof["launches"] / max(ROOF_STEPS, 1)
+    if per_step <= 2.5:
+        kernel = ("k_layers, the layer stack (q|k|v + RoPE + K/V append, attention, o + residual, gate|up + SiLU, down + residual "
+                  "of every layer in one launch), and k_head")
+        traffic_path = os.path.join(ROOT, "profiles", f"k_layers_{tag}_verify_hbm_traffic.md")
+    else:
+        kernel = "per-layer matrix launches (q|k|v, attention + o, gate|up, down) and the head"
+        traffic_path = os.path.join(ROOT, "profiles", f"k_mm_{tag}_verify_hbm_traffic.md")
+    roofline = roofline_of(prof, f"{kernel}; MFMA weight streaming, {FMT_NAME[conf['fmt'][0]]}, t={k + 1}", traffic_path)
     res = {
         "metric": METRIC,
         "value": round(value, 2),

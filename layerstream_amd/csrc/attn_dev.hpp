@@ -25,7 +25,9 @@ namespace ls {
 // (workgroup (b % (AWV ASPLIT)) / AWV), which keeps a running (max, sum, output) per token over its
 // blocks in order (online softmax) without any barrier: the scores ([keys][tokens]) and the
 // weighted sum ([dims][tokens]) run on v_mfma_f32_16x16x4f32 straight from registers, each lane
-// loading the K, V and q values it feeds (the next block's while this one computes). The AWV
+// loading the K, V and q values it feeds. With AWV ASPLIT = 64 wavefronts per (head, segment) a
+// wavefront owns at most a few blocks at these contexts, so one block's registers are loaded at a
+// time: the second buffer would cost the occupancy that batched launches need. The AWV
 // wavefronts' states merge in LDS in wavefront order, and the last of the ASPLIT workgroups to
 // finish (an agent-scope counter) merges theirs in workgroup order and writes the output rows as
 // fragments. Which blocks a wavefront takes depends only on key positions, so a token's result
@@ -229,7 +231,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     const __amdgpu_buffer_rsrc_t rl = coherent_rsrc(pl, rows_total * ASPLIT * 4);
     const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(po, rows_total * ASPLIT * HD * 4);
 
-    AttnBlock<HD> ba, bb;
+    AttnBlock<HD> ba;
     float qr[H4];
     // Blocks below nold hold only keys cached before this launch (every block without IN_FLOW).
     const int nold = IN_FLOW ? *A.pos0p / AKB : nb;
@@ -301,12 +303,9 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
             for (int i = 0; i < 4; i++) O[db][i] = __builtin_fmaf(O[db][i], corr, acc[i]);
         }
     };
-    for (int b = first; b < nb; b += 2 * stride) {
-        if (b + stride < nb) load_block(bb, b + stride);
+    for (int b = first; b < nb; b += stride) {
+        if (b != first) load_block(ba, b);
         block(b, ba);
-        if (b + stride >= nb) break;
-        if (b + 2 * stride < nb) load_block(ba, b + 2 * stride);
-        block(b + stride, bb);
     }
 
     // The AWV wavefronts' states, merged in wavefront order into this workgroup's state.
