@@ -1061,22 +1061,22 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     const int NC = W.n_chunks, F = my_groups * NC;
     const size_t sst = size_t(NC) * 1024;
     auto wbase = [&](int f) { return W.data + (size_t(4 * (first + (f / NC) * stride)) * NC * 64 + lane) * 16; };
-    // The tile's fragments (at most HEAD_BMAX per thread) are requested before the weight
-    // chunks: a wavefront's loads complete in order, so they reach LDS at L2 latency instead of
-    // waiting behind the HBM stream.
+    // The tile's fragments (at most HEAD_BMAX slots per thread) go straight to LDS, requested
+    // before the weight chunks; staged through registers they would spill. The wait for them
+    // also covers the first HEAD_PF chunks, which the first MFMAs need anyway.
     const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
     const int nb = nks * 3 * 64, nthr = 64 * HEAD_WAVES;
-    uint4 bv[HEAD_BMAX];
-#pragma unroll
-    for (int u = 0; u < HEAD_BMAX; u++)
-        if (int(threadIdx.x) + u * nthr < nb) bv[u] = fb[threadIdx.x + u * nthr];
+    // A wavefront moves 64 slots of 16 bytes per load.
+    for (int u = 0; u < HEAD_BMAX; u++) {
+        const int w0 = wv * 64 + u * nthr;  // this wavefront's first slot; nb is a multiple of 64
+        if (w0 >= nb) break;
+        __builtin_amdgcn_global_load_lds(fb + w0 + lane, (__attribute__((address_space(3))) void*)(bl + w0), 16, 0, 0);
+    }
     uint4 raw[HEAD_PF][4];
 #pragma unroll
     for (int p = 0; p < HEAD_PF; p++)
         if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
-#pragma unroll
-    for (int u = 0; u < HEAD_BMAX; u++)
-        if (int(threadIdx.x) + u * nthr < nb) bl[threadIdx.x + u * nthr] = bv[u];
+    __builtin_amdgcn_s_waitcnt(0);
     if (wv == 0) {
         if (a.ss) inv_rms(a, tile, W.cols, inv);
         else if (lane < FTOK) inv[lane] = 1.0f;
