@@ -5,6 +5,7 @@ Tolerances: logits within 1e-4 * (1 + max|ref|) on the tiny models and 1e-3 rela
 Within the GPU engine, batched and single-token passes, and resident and streamed weights, are
 compared bit for bit.
 """
+import contextlib
 import os
 import sys
 
@@ -438,6 +439,43 @@ def verify_step_vs_oracle(m, prompt, k, rng, max_ctx, tag):
     while want_m < k and ref[want_m].argmax() == drafts[want_m]:
         want_m += 1
     assert acc == want_m >= 2 and nxt == ref[want_m].argmax()
+
+
+@contextlib.contextmanager
+def env(name, value):
+    """An engine switch read when a model is created."""
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        yield
+    finally:
+        if old is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = old
+
+
+def test_layer_stack_and_per_layer_launches_give_identical_bits():
+    """One-tile passes run every layer in one launch (k_layers) by default; LS_STACK=0 runs the
+    per-layer launches. Same plans, so the same logits bit for bit, and the same acceptance."""
+    block = [8, 9, 400, 33, 120, 5, 77, 301, 2]
+    cases = [(name, tiny(name), PROMPT, 128) for name in ("bf16", "int8", "int4")]
+    rng = np.random.default_rng(3)
+    cases.append(("0.5B int8", qwen05b((8, 64)), rng.integers(0, 151936, 40).tolist(), 256))
+    for name, m, prompt, max_ctx in cases:
+        say("stack vs per-layer", name)
+        with env("LS_STACK", "0"):
+            a = gpu_model(m, max_ctx=max_ctx)
+        b = gpu_model(m, max_ctx=max_ctx)
+        la, lb = a.forward(prompt), b.forward(prompt)
+        assert np.array_equal(bits(la), bits(lb)), name
+        p = a.pos()
+        va, vb = a.forward_multi(block, len(block)), b.forward_multi(block, len(block))
+        assert np.array_equal(bits(va), bits(vb)), name
+        a.truncate(p)
+        b.truncate(p)
+        assert a.verify_greedy(block) == b.verify_greedy(block), name
+        assert a.pos() == b.pos()
 
 
 def test_qwen3b_int8_verify_step_matches_the_oracle():
