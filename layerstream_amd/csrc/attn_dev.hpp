@@ -189,8 +189,13 @@ inline AttnArgs make_attn_args(const float* q, int ldq, int t, int heads, int kv
 // With IN_FLOW (one sequence) q and the keys from the launch's first position on are written by
 // earlier workgroups of the same launch: the workgroup loads its first block if it holds only
 // older keys, waits on fin (counter `head`), then reads q and newer keys coherently.
+// LDS of one attention workgroup: per-wavefront (max, sum) and outputs, then a flag.
+template <int HD>
+__host__ __device__ constexpr size_t attn_lds_bytes() { return size_t(2 * AWV * ATQ + AWV * ATQ * (HD + 4)) * 4 + 16; }
+
 template <int HD, bool OUT_FLOW, bool IN_FLOW = false>
-__device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, int seg, const Flow& fl, const Flow& fin = Flow{}) {
+__device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, int seg, const Flow& fl, uint8_t* smem,
+                                          const Flow& fin = Flow{}) {
     const float* __restrict__ q = A.q;
     const int ldq = A.ldq, t = A.t, heads = A.heads, kv_heads = A.kv_heads;
     const AttnRows& rows = A.rows;
@@ -203,10 +208,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     uint8_t* __restrict__ frags = A.frags;
     const size_t frag_stride = A.frag_stride;
     constexpr int H4 = HD / 4, DB = HD / 16;
-    __shared__ float sm_m[AWV][ATQ], sm_l[AWV][ATQ];
+    // In the workgroup's LDS (attn_lds_bytes<HD>() from smem; a fused launch shares it with its
+    // matrix roles, one role per workgroup).
+    float(*sm_m)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem);
+    float(*sm_l)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem + AWV * ATQ * 4);
     constexpr int HP = HD + 4;  // padded row of the wavefront outputs
-    __shared__ __align__(16) float sm_o[AWV * ATQ * HP];  // wavefront outputs [wave][token][dim], then the output rows
-    __shared__ int flag;
+    float* sm_o = reinterpret_cast<float*>(smem + 2 * AWV * ATQ * 4);  // wavefront outputs [wave][token][dim], then the output rows
+    int& flag = *reinterpret_cast<int*>(smem + 2 * AWV * ATQ * 4 + AWV * ATQ * HP * 4);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
     const int kv = kv_heads * HD, col0 = (head / (heads / kv_heads)) * HD;
     int i0, nq, pos_first;  // first launch row, rows, position of the first row

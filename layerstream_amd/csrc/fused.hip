@@ -483,8 +483,8 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     float* xs = reinterpret_cast<float*>(bi + FTOK * 16);
     float* vec = xs + rows_wg * FTOK;
     float* rcos = vec + rows_wg;
-    float* rsin = rcos + FTOK * ROPE_HALF_MAX;
-    int* tpos = reinterpret_cast<int*>(rsin + FTOK * ROPE_HALF_MAX);  // [position][cache row] per token
+    float* rsin = rcos + FTOK * (EPI == EPI_QKV ? a.hd / 2 : 0);
+    int* tpos = reinterpret_cast<int*>(rsin + FTOK * (EPI == EPI_QKV ? a.hd / 2 : 0));  // [position][cache row] per token
     const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
 
     // Every load of the wavefront's share is issued before any arithmetic.
@@ -880,7 +880,7 @@ __global__ __launch_bounds__(512) void k_attn_o(AttnArgs aa, MMArgs o, MMPlan po
     const int na = ASPLIT * aa.heads;
     if (int(blockIdx.x) < na) {
         if (int(threadIdx.x) >= AWV * 64) return;
-        attn_body<HD, true>(aa, int(blockIdx.x) % ASPLIT, int(blockIdx.x) / ASPLIT, 0, fl);
+        attn_body<HD, true>(aa, int(blockIdx.x) % ASPLIT, int(blockIdx.x) / ASPLIT, 0, fl, smem);
     } else {
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
         mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fl, Flow{}, int(blockIdx.x) - na, 0, smem);
@@ -901,7 +901,7 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
         mm_body<BITS, EPI_QKV, G16, 1, false, true>(qa, pq, sc, Flow{}, fq, bid, 0, smem);
     } else if (bid < nq + na) {
         if (int(threadIdx.x) >= AWV * 64) return;
-        attn_body<HD, true, true>(aa, (bid - nq) % ASPLIT, (bid - nq) / ASPLIT, 0, fo, fq);
+        attn_body<HD, true, true>(aa, (bid - nq) % ASPLIT, (bid - nq) / ASPLIT, 0, fo, smem, fq);
     } else {
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
         mm_body<BITS, EPI_RESID, G16, 1, true, false>(o, po, sc, fo, Flow{}, bid - nq - na, 0, smem);
@@ -971,7 +971,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.consumers = no;
         fout.base = base + FL_A;
         fout.mirrors = lf.m_a;
-        attn_body<HD, true, true>(A, r % ASPLIT, r / ASPLIT, 0, fout, fin);
+        attn_body<HD, true, true>(A, r % ASPLIT, r / ASPLIT, 0, fout, smem, fin);
         return;
     }
     r -= na;
@@ -1210,10 +1210,12 @@ size_t mm_part_floats(const MMPlan& p) {
 }
 size_t mm_counters(const MMPlan& p) { return p.nsplit > 1 ? size_t(p.tiles) * p.nrb : 0; }
 
-static size_t lds_bytes(const MMPlan& p) {
+// LDS of a matrix workgroup (the layout at the top of mm_body); hd: head_dim of a q|k|v matrix
+// (its RoPE tables), 0 for the others.
+static size_t lds_bytes(const MMPlan& p, int hd = 0) {
     const size_t red = p.kw > 1 ? size_t(p.rg) * p.kw * p.s * 64 * 16 : 0;
     const size_t rows = size_t(16 * p.s * p.rg);
-    return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * ROPE_HALF_MAX + 2 * FTOK) * 4;
+    return red + rows * FTOK * 4 + FTOK * 4 + 16 + FTOK * 16 * 8 + (rows * FTOK + rows + 2 * FTOK * size_t(hd / 2) + 2 * FTOK) * 4;
 }
 
 static thread_local hipEvent_t t_start = nullptr, t_stop = nullptr;
@@ -1239,7 +1241,7 @@ static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStr
     if (p.s != S) throw std::runtime_error("matrix plan does not match the kernel's strips per wavefront");
     if (p.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
     const dim3 grid(p.nrb * p.nsplit, p.tiles), block(64 * p.rg * p.kw);
-    const size_t lds = lds_bytes(p);
+    const size_t lds = lds_bytes(p, EPI == EPI_QKV ? a.hd : 0);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
     switch (a.W.bits) {
         case 16: go(k_mm<16, EPI, false, S>, grid, block, lds, s, a, p, sc); break;
@@ -1315,7 +1317,7 @@ int attention_o_workgroups(int heads, const MMPlan& po) { return ASPLIT * heads 
 template <int HD>
 static void launch_attn_o(const AttnArgs& aa, const MMArgs& o, const MMPlan& po, const MMScratch& sc, const Flow& fl, hipStream_t s) {
     const dim3 grid(attention_o_workgroups(aa.heads, po)), block(std::max(AWV * 64, 64 * po.rg * po.kw));
-    const size_t lds = lds_bytes(po);
+    const size_t lds = std::max(lds_bytes(po), attn_lds_bytes<HD>());
     const bool g16 = o.W.bits != 16 && o.W.group == 16;
     switch (o.W.bits) {
         case 16: go(k_attn_o<HD, 16, false>, grid, block, lds, s, aa, o, po, sc, fl); break;
@@ -1362,7 +1364,7 @@ template <int HD>
 static void launch_qkv_attn_o(const MMArgs& qa, const MMPlan& pq, const AttnArgs& aa, const MMArgs& o, const MMPlan& po, const MMScratch& sc,
                               const Flow& fq, const Flow& fo, hipStream_t s) {
     const dim3 grid(qkv_attention_o_workgroups(aa.heads, pq, po)), block(std::max({AWV * 64, 64 * po.rg * po.kw, 64 * pq.rg * pq.kw}));
-    const size_t lds = std::max(lds_bytes(pq), lds_bytes(po));
+    const size_t lds = std::max({lds_bytes(pq, qa.hd), lds_bytes(po), attn_lds_bytes<HD>()});
     const bool g16 = o.W.bits != 16 && o.W.group == 16;
     switch (o.W.bits) {
         case 16: go(k_qkv_attn_o<HD, 16, false>, grid, block, lds, s, qa, pq, aa, o, po, sc, fq, fo); break;
@@ -1441,7 +1443,11 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
                           const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da, const MMPlan& pd,
                           const MMScratch& sc, const LayerFlows& lf, hipStream_t s) {
     const dim3 grid(layers * layer_stack_workgroups(aa.heads, pq, po, pg, pd)), block(512);
-    const size_t lds = std::max({lds_bytes(pq), lds_bytes(po), lds_bytes(pg), lds_bytes(pd)});
+    // int8 layers run one workgroup per CU (asking for more than half its LDS): their passes are
+    // bound by handoff latency, and twice the resident workgroups poll twice as much (C2: 0.90 ms
+    // per step at one, 0.97 at two). bf16 and int4 layers gain from the wider window (two).
+    const size_t lds = std::max({lds_bytes(pq, qa.hd), lds_bytes(po), lds_bytes(pg), lds_bytes(pd), attn_lds_bytes<HD>(),
+                                 qa.W.bits == 8 ? size_t(96) << 10 : size_t(0)});
     const bool g16 = qa.W.bits != 16 && qa.W.group == 16;
     switch (qa.W.bits) {
         case 16: go(k_layers<HD, 16, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;

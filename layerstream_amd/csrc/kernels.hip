@@ -24,7 +24,8 @@ namespace ls {
 
 template <int HD>
 __global__ __launch_bounds__(AWV * 64) void k_attn(AttnArgs a) {
-    attn_body<HD, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, Flow{});
+    __shared__ __align__(16) uint8_t smem[attn_lds_bytes<HD>()];
+    attn_body<HD, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, Flow{}, smem);
 }
 
 size_t attention_scratch_floats(int t, int heads, int hd, int) { return size_t(t) * heads * ASPLIT * (hd + 2); }
