@@ -1443,11 +1443,11 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
                           const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da, const MMPlan& pd,
                           const MMScratch& sc, const LayerFlows& lf, hipStream_t s) {
     const dim3 grid(layers * layer_stack_workgroups(aa.heads, pq, po, pg, pd)), block(512);
-    // int8 layers run one workgroup per CU (asking for more than half its LDS): their passes are
-    // bound by handoff latency, and twice the resident workgroups poll twice as much (C2: 0.90 ms
-    // per step at one, 0.97 at two). bf16 and int4 layers gain from the wider window (two).
+    // One workgroup per CU (the launch asks for more than half its LDS): a pass is bound by
+    // handoff latency, and twice the resident workgroups poll twice as much (0.5B int8: 0.89 ms
+    // per step at one, 0.97 at two; int4: 1.01 and 1.18).
     const size_t lds = std::max({lds_bytes(pq, qa.hd), lds_bytes(po), lds_bytes(pg), lds_bytes(pd), attn_lds_bytes<HD>(),
-                                 qa.W.bits == 8 ? size_t(96) << 10 : size_t(0)});
+                                 size_t(96) << 10});
     const bool g16 = qa.W.bits != 16 && qa.W.group == 16;
     switch (qa.W.bits) {
         case 16: go(k_layers<HD, 16, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;

@@ -57,13 +57,12 @@ __host__ __device__ inline size_t frag_tile_bytes(int cols) { return size_t(tile
 // Sum-of-squares slots (16 columns each) of a row of `cols` values.
 __host__ __device__ inline int ss_slots(int cols) { return (cols + 15) / 16; }
 // gate|up rows are interleaved in blocks of 16 * GU_STRIPS (gate block, up block, ...). A
-// workgroup row group holds a gate block and its up block. For int8 (groups of 32+) one
-// wavefront streams both (4 strips), so the input fragments it loads serve both: that launch is
-// bound by fragment loads. bf16 and groups of 16 need the registers for their wider chunks or
-// extra MFMAs, and int4 is bound by its per-wavefront MFMA and unpack chain, so those use two
-// wavefronts of one block each.
+// workgroup row group holds a gate block and its up block. One wavefront streams both (4 strips),
+// so the input fragments it loads serve both, and a workgroup of 7 wavefronts along K fits the
+// layer stack's 512 threads. Groups of 16 need the registers for their extra MFMAs, so they use
+// two wavefronts of one block each.
 constexpr int GU_STRIPS = 2;
-__host__ __device__ constexpr int gu_wave_strips(int bits, int group) { return (bits == 8 && group != 16) ? 2 * GU_STRIPS : GU_STRIPS; }
+__host__ __device__ constexpr int gu_wave_strips(int bits, int group) { return (bits == 16 || group != 16) ? 2 * GU_STRIPS : GU_STRIPS; }
 // Strips per wavefront of the down projection: its K (the FFN width) is long and its rows few,
 // so two strips halve the input-fragment reads per weight byte.
 constexpr int DOWN_STRIPS = 2;
