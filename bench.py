@@ -363,7 +363,7 @@ def run_single(args, conf):
     # Per-launch timing of the matrix kernels: HIP events on the compute stream around every
     # launch, over ROOF_STEPS further verify steps of the same run (kept out of the timed steps,
     # whose launches they would space out).
-    model.profile(True)
+    model.profile(True, dominant=True)
     run.step(ROOF_STEPS)
     hip_sync()
     prof = model.profile_read()
@@ -381,9 +381,9 @@ def run_single(args, conf):
     step_ms_p50 = float(np.median(tms))
     tag = model_tag(conf)
     per_step = prof["launches"] / max(ROOF_STEPS, 1)
-    if per_step <= 2.5:
+    if per_step <= 1.5:
         kernel = ("k_layers, the layer stack (q|k|v + RoPE + K/V append, attention, o + residual, gate|up + SiLU, down + residual "
-                  "of every layer in one launch), and k_head")
+                  "of every layer in one launch), the dominant kernel of the step")
         traffic_path = os.path.join(ROOT, "profiles", f"k_layers_{tag}_verify_hbm_traffic.md")
     else:
         kernel = "per-layer matrix launches (q|k|v, attention + o, gate|up, down) and the head"

@@ -176,7 +176,9 @@ double ls_model_last_step_ms(const ls_model* m);
 /* Profiling of the weight-streaming matvec kernels: with enable != 0, HIP events bracket each
  * launch on the model's compute stream; ls_model_profile_read returns the launches, their summed
  * device time and their algorithmic bytes (weights in the stored format + f32 inputs + f32
- * outputs) since the last read, then resets. */
+ * outputs) since the last read, then resets. enable = 1 takes every matrix launch; enable = 2 only
+ * each pass's dominant launch: the layer stack when a pass runs every layer in one launch (the
+ * head is left out), else every matrix launch. */
 typedef struct {
     uint64_t launches;
     double ms;

@@ -414,9 +414,10 @@ class Model:
     def last_step_ms(self) -> float:
         return lib().ls_model_last_step_ms(self.h)
 
-    def profile(self, enable: bool):
-        """Bracket every weight-streaming matvec launch with HIP events (for roofline figures)."""
-        _check(lib().ls_model_profile(self.h, int(enable)))
+    def profile(self, enable: bool, dominant: bool = False):
+        """Bracket every weight-streaming matvec launch with HIP events (for roofline figures);
+        with dominant, only each pass's dominant launch (the layer stack when a pass runs as one)."""
+        _check(lib().ls_model_profile(self.h, (2 if dominant else 1) if enable else 0))
 
     def profile_read(self) -> dict:
         st = KernelStat()

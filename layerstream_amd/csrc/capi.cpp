@@ -386,7 +386,7 @@ void ls_spec_free(ls_spec* s) { delete s; }
 int ls_model_profile(ls_model* m, int enable) {
     return guard([&] {
         need(m, "model");
-        m->m->set_profiling(enable != 0);
+        m->m->set_profiling(enable == 2 ? 2 : (enable != 0 ? 1 : 0));
     });
 }
 

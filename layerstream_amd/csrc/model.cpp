@@ -602,7 +602,7 @@ void Model::check_request(const uint32_t* tok, size_t n) const {
 // ---- profiling of the weight-streaming kernels ------------------------------------------
 // The next matrix launch records its own start and end (no marker packets in between).
 void Model::prof_begin() {
-    if (!prof_) return;
+    if (!prof_ || prof_skip_) return;
     while (prof_ev_.size() < prof_used_ + 2) {
         hipEvent_t e;
         HIPC(hipEventCreate(&e));
@@ -612,7 +612,7 @@ void Model::prof_begin() {
 }
 
 void Model::prof_end(const TMat& W, int nt, bool launch, double extra_bytes) {
-    if (!prof_) return;
+    if (!prof_ || prof_skip_) return;
     const Format f{W.bits, W.group};
     if (launch) {
         prof_used_ += 2;
@@ -636,7 +636,7 @@ void Model::set_graphs(bool on) {
     graphs_on_ = on;
 }
 
-void Model::set_profiling(bool on) {
+void Model::set_profiling(int on) {
     HIPC(hipStreamSynchronize(stream_));
     harvest();
     prof_ = on;
@@ -702,6 +702,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     const DevLayer* L0 = res ? &prov_->layer(0) : nullptr;
     prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr);
     bool stacked = false;
+    prof_skip_ = false;
     if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
         // One launch for every layer: the same plans (so the same bits) as the per-layer
         // launches below.
@@ -770,6 +771,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             stacked = true;
         }
     }
+    // The dominant launch of a stacked pass is the stack itself.
+    prof_skip_ = stacked && prof_ == 2;
     for (size_t l = 0; !stacked && l < c.layers; l++) {
         const DevLayer& L = prov_->layer(l);
         // This layer's caches: every sequence's for a batch, else the selected one's.
@@ -950,7 +953,9 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
         }
         head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(),
                           accept_block, reinterpret_cast<uint32_t*>(ctl_.as<int>() + FLOW_ACC), s);
+
     }
+    prof_skip_ = false;
     prov_->end_forward();
     if (!bv) pos_ += t;
 }

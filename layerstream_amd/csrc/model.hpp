@@ -133,7 +133,9 @@ public:
     ls_report report() const { return prov_->report(); }
     double last_step_ms() const { return last_step_ms_; }
     int device() const { return device_; }
-    void set_profiling(bool on);
+    // mode 0: off; 1: every matrix launch; 2: each pass's dominant launch (the layer stack when a
+    // pass runs as one, else every matrix launch).
+    void set_profiling(int mode);
     void set_graphs(bool on);
     ls_kernel_stat read_profile();
 
@@ -189,7 +191,8 @@ private:
     int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 8, kw_head_ = 7;
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
-    bool prof_ = false;
+    int prof_ = 0;  // profiling mode (set_profiling)
+    bool prof_skip_ = false;  // launches of this pass outside the profiled set
     bool graphs_on_ = true;
     std::map<std::pair<int, size_t>, hipGraphExec_t> graphs_;  // verify step per (sequence, block length)
     std::map<std::vector<size_t>, hipGraphExec_t> batch_graphs_;  // batched verify step per block lengths
