@@ -222,10 +222,19 @@ class StreamProvider : public DeviceProvider {
         size_t idx;
         bool operator==(const Item& o) const { return kind == o.kind && idx == o.idx; }
     };
+    // A device slot: an item in the tile layout, as compute reads it.
     struct Slot {
-        DevBuf raw, arena, hdata, hscales;
+        DevBuf arena, hdata, hscales;
+        hipEvent_t ready = nullptr, freed = nullptr;
+        bool used = false;
+    };
+    // A landing buffer for one item's bytes as the source holds them (reference layout). There is
+    // one more than there are slots, so a copy never waits for the rearrangement of the item just
+    // before it.
+    struct Landing {
+        DevBuf raw;
         PinnedBuf stage;
-        hipEvent_t copied = nullptr, ready = nullptr, freed = nullptr;
+        hipEvent_t copied = nullptr, consumed = nullptr;
         bool used = false;
     };
 
@@ -241,16 +250,20 @@ public:
         hshape_ = tile_shape(ef.bits, ef.group, int(STREAM_HEAD_ROWS), int(c_.hidden), 256);
         slots_.resize(size_t(slots));
         for (auto& s : slots_) {
-            s.raw = DevBuf(buf_size_);
             s.arena = DevBuf(a_.total);
             clear_layer(a_, s.arena.as<uint8_t>(), copy_);
             s.hdata = DevBuf(tile_data_bytes(hshape_));
             s.hscales = DevBuf(std::max<size_t>(16, tile_scale_bytes(hshape_)));
             tile_clear(tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>()), copy_);
-            if (!src_.pinned()) s.stage = PinnedBuf(buf_size_);
-            HIPC(hipEventCreateWithFlags(&s.copied, hipEventDisableTiming));
             HIPC(hipEventCreateWithFlags(&s.ready, hipEventDisableTiming));
             HIPC(hipEventCreateWithFlags(&s.freed, hipEventDisableTiming));
+        }
+        landing_.resize(size_t(slots) + 1);
+        for (auto& d : landing_) {
+            d.raw = DevBuf(buf_size_);
+            if (!src_.pinned()) d.stage = PinnedBuf(buf_size_);
+            HIPC(hipEventCreateWithFlags(&d.copied, hipEventDisableTiming));
+            HIPC(hipEventCreateWithFlags(&d.consumed, hipEventDisableTiming));
         }
         HIPC(hipStreamSynchronize(copy_));
         embed_stage_ = PinnedBuf(max_rows_ * rb);
@@ -262,9 +275,12 @@ public:
         (void)hipStreamSynchronize(build_);
         (void)hipStreamSynchronize(compute_);
         for (auto& s : slots_) {
-            (void)hipEventDestroy(s.copied);
             (void)hipEventDestroy(s.ready);
             (void)hipEventDestroy(s.freed);
+        }
+        for (auto& d : landing_) {
+            (void)hipEventDestroy(d.copied);
+            (void)hipEventDestroy(d.consumed);
         }
         (void)hipEventDestroy(embed_copied_);
         (void)hipStreamDestroy(build_);
@@ -273,14 +289,19 @@ public:
     const char* name() const override { return "stream"; }
 
     void begin_forward(bool with_head) override {
-        // Recover from an earlier pass that stopped early: wait for copies in flight.
-        HIPC(hipStreamSynchronize(copy_));
-        HIPC(hipStreamSynchronize(build_));
+        // Items the previous pass issued ahead for this one (its first layers) are in flight;
+        // otherwise (an earlier pass stopped early) wait for whatever copies are.
+        if (!ahead_) {
+            HIPC(hipStreamSynchronize(copy_));
+            HIPC(hipStreamSynchronize(build_));
+        }
         schedule_.clear();
         for (size_t l = 0; l < c_.layers; l++) schedule_.push_back({LAYER, l});
         if (with_head)
             for (size_t c = 0; c < n_head_chunks(); c++) schedule_.push_back({HEAD, c});
-        next_issue_ = next_take_ = 0;
+        next_issue_ = ahead_;
+        next_take_ = 0;
+        ahead_ = 0;
         holding_ = false;
         while (next_issue_ < schedule_.size() && next_issue_ < slots_.size()) issue();
     }
@@ -292,6 +313,7 @@ public:
     }
     void release_layer(size_t) override { release(); }
     size_t n_head_chunks() const override { return (c_.vocab + STREAM_HEAD_ROWS - 1) / STREAM_HEAD_ROWS; }
+    size_t head_rows(size_t c) const { return std::min(STREAM_HEAD_ROWS, c_.vocab - c * STREAM_HEAD_ROWS); }
     HeadChunk head_chunk(size_t c) override {
         Slot& s = take({HEAD, c});
         const size_t first = c * STREAM_HEAD_ROWS, rows = std::min(STREAM_HEAD_ROWS, c_.vocab - first);
@@ -304,6 +326,16 @@ public:
         if (holding_) release();
         if (next_take_ != schedule_.size())
             fail("forward pass ended before every scheduled item was consumed", LS_E_STATE);
+        // Every pass starts with the same layers, whatever it asks for: with the bytes already in
+        // pinned host memory, their copies start now instead of after the host has seen this
+        // pass's result. (Other sources read from storage, counted at the read: they wait.)
+        if (src_.pinned()) {
+            schedule_.clear();
+            for (size_t l = 0; l < c_.layers && l < slots_.size(); l++) schedule_.push_back({LAYER, l});
+            next_issue_ = 0;
+            while (next_issue_ < schedule_.size()) issue();
+            ahead_ = next_issue_;
+        }
     }
 
     bool resident() const override { return false; }
@@ -321,7 +353,8 @@ public:
 
     ls_report report() const override {
         ls_report r{};
-        for (auto& s : slots_) r.resident_weight_bytes += s.raw.n + s.arena.n + s.hdata.n + s.hscales.n;
+        for (auto& s : slots_) r.resident_weight_bytes += s.arena.n + s.hdata.n + s.hscales.n;
+        for (auto& d : landing_) r.resident_weight_bytes += d.raw.n;
         r.bytes_read = src_.bytes_read();
         r.wait_ns = wait_ns_;
         r.h2d_bytes = h2d_bytes_;
@@ -332,6 +365,7 @@ private:
     void issue() {
         const Item it = schedule_[next_issue_];
         Slot& s = slots_[next_issue_ % slots_.size()];
+        Landing& d = landing_[next_issue_ % landing_.size()];
         const size_t rb = c_.row_bytes();
         size_t bytes, first = 0, rows = 0;
         if (it.kind == LAYER) {
@@ -344,33 +378,35 @@ private:
         const uint8_t* from;
         if (src_.pinned()) {
             from = it.kind == LAYER ? src_.layer_view(it.idx) : src_.embed_view() + first * rb;
-            src_.count_read(bytes);
         } else {
             auto t0 = std::chrono::steady_clock::now();
-            HIPC(hipEventSynchronize(s.copied));  // the staging buffer's previous copy has landed
+            HIPC(hipEventSynchronize(d.copied));  // the staging buffer's previous copy has landed
             wait_ns_ += uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count());
-            if (it.kind == LAYER) src_.read_layer(it.idx, s.stage.as<uint8_t>());
-            else src_.read_embed_rows(first, rows, s.stage.as<uint8_t>());
-            from = s.stage.as<uint8_t>();
+            if (it.kind == LAYER) src_.read_layer(it.idx, d.stage.as<uint8_t>());
+            else src_.read_embed_rows(first, rows, d.stage.as<uint8_t>());
+            from = d.stage.as<uint8_t>();
         }
-        // The raw buffer is free once the previous item's build has read it; the arena once the
-        // compute stream is done with that item. The copy waits only for the former.
-        if (s.used) HIPC(hipStreamWaitEvent(copy_, s.ready, 0));
-        HIPC(hipMemcpyAsync(s.raw.p, from, bytes, hipMemcpyHostToDevice, copy_));
+        // The landing buffer is free once the rearrangement of its previous item has read it
+        // (slots + 1 items back); the slot's arena once the compute stream is done with its
+        // previous item. The copy waits only for the former.
+        if (d.used) HIPC(hipStreamWaitEvent(copy_, d.consumed, 0));
+        HIPC(hipMemcpyAsync(d.raw.p, from, bytes, hipMemcpyHostToDevice, copy_));
         h2d_bytes_ += bytes;
-        HIPC(hipEventRecord(s.copied, copy_));
+        HIPC(hipEventRecord(d.copied, copy_));
         // The tile layout is built on a stream of its own, so the next item's PCIe copy runs
         // meanwhile.
-        HIPC(hipStreamWaitEvent(build_, s.copied, 0));
+        HIPC(hipStreamWaitEvent(build_, d.copied, 0));
         if (s.used) HIPC(hipStreamWaitEvent(build_, s.freed, 0));
         if (it.kind == LAYER) {
-            build_layer_device(c_, L_, s.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), build_);
+            build_layer_device(c_, L_, d.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), build_);
         } else {
             TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
-            tile_repack(s.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), build_);
+            tile_repack(d.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), build_);
         }
         HIPC(hipEventRecord(s.ready, build_));
+        HIPC(hipEventRecord(d.consumed, build_));
         s.used = true;
+        d.used = true;
         next_issue_++;
     }
 
@@ -382,6 +418,8 @@ private:
                  LS_E_STATE);
         Slot& s = slots_[next_take_ % slots_.size()];
         HIPC(hipStreamWaitEvent(compute_, s.ready, 0));
+        // Pinned bytes are counted when the pass takes them (they may be copied a pass ahead).
+        if (src_.pinned()) src_.count_read(want.kind == LAYER ? L_.total : head_rows(want.idx) * c_.row_bytes());
         holding_ = true;
         return s;
     }
@@ -402,8 +440,10 @@ private:
     TMat hshape_;
     hipStream_t compute_, copy_ = nullptr, build_ = nullptr;
     std::vector<Slot> slots_;
+    std::vector<Landing> landing_;
     std::vector<Item> schedule_;
     size_t next_issue_ = 0, next_take_ = 0, buf_size_ = 0;
+    size_t ahead_ = 0;  // items of the next pass issued at the end of the last one
     bool holding_ = false;
     DevLayer cur_layer_;
     size_t max_rows_;
