@@ -302,10 +302,15 @@ __device__ __forceinline__ f32x4 mfma3(const uint4& A, const uint4* B, f32x4 c) 
     return c;
 }
 
-__device__ __forceinline__ f32x4 scales4(const uint16_t* __restrict__ sc, int strip, int n_groups, int g, int lane) {
-    const uint2 v = *reinterpret_cast<const uint2*>(sc + (size_t(strip) * n_groups + g) * 16 + 4 * (lane >> 4));
+__device__ __forceinline__ uint2 scales_raw(const uint16_t* __restrict__ sc, int strip, int n_groups, int g, int lane) {
+    return *reinterpret_cast<const uint2*>(sc + (size_t(strip) * n_groups + g) * 16 + 4 * (lane >> 4));
+}
+__device__ __forceinline__ f32x4 scales_f32(uint2 v) {
     return f32x4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
                  __uint_as_float(v.y & 0xffff0000u)};
+}
+__device__ __forceinline__ f32x4 scales4(const uint16_t* __restrict__ sc, int strip, int n_groups, int g, int lane) {
+    return scales_f32(scales_raw(sc, strip, n_groups, g, lane));
 }
 
 // Chunks per wavefront: every wavefront covers 4 k-steps (128 columns).
@@ -327,9 +332,40 @@ __device__ __forceinline__ void load_chunk(const uint8_t* base, size_t sstride, 
 
 // One chunk: Q k-steps x S strips x 3 MFMAs, with group scaling. B[q][term] are the fragments of
 // the chunk's k-steps; [ks_begin, ks_end) is the wavefront's k-step range.
+// Scale slots per chunk (k-steps that may close a group; groups of 16: two per k-step).
+template <int BITS, bool G16>
+constexpr int scale_slots() {
+    return BITS == 16 ? 1 : (G16 ? 2 * Steps<BITS>::Q : Steps<BITS>::Q);
+}
+
+// The group scales chunk_mfma applies for chunk c, loaded ahead (with the weights): the same
+// scales, so the products are unchanged, but their latency no longer follows the input's.
 template <int BITS, bool G16, int S>
+__device__ __forceinline__ void load_scales(const TMat& W, int s0, int c, int ks_end, uint2 (*scl)[S]) {
+    const int lane = threadIdx.x & 63;
+    constexpr int Q = Steps<BITS>::Q;
+    const int G = W.group;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int ks = c * Q + q;
+        if constexpr (G16) {
+#pragma unroll
+            for (int r = 0; r < S; r++) {
+                scl[2 * q][r] = scales_raw(W.scales, s0 + r, W.n_groups, 2 * ks, lane);
+                scl[2 * q + 1][r] = scales_raw(W.scales, s0 + r, W.n_groups, 2 * ks + 1, lane);
+            }
+        } else {
+            const bool last = ((ks + 1) * 32) % G == 0 || ks == ks_end - 1;
+#pragma unroll
+            for (int r = 0; r < S; r++) scl[q][r] = last ? scales_raw(W.scales, s0 + r, W.n_groups, ks * 32 / G, lane) : make_uint2(0, 0);
+        }
+    }
+}
+
+// With PRE the scales come from scl (load_scales for this chunk), else from memory here.
+template <int BITS, bool G16, int S, bool PRE = false>
 __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_begin, int ks_end, const uint4 (*B)[3],
-                                           const uint4* raw, f32x4* acc, f32x4* total) {
+                                           const uint4* raw, f32x4* acc, f32x4* total, const uint2 (*scl)[S] = nullptr) {
     const int lane = threadIdx.x & 63;
     constexpr int Q = Steps<BITS>::Q;
     const int G = W.group;
@@ -348,7 +384,7 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
                 const int g = ks * 32 / G;
 #pragma unroll
                 for (int r = 0; r < S; r++) {
-                    const f32x4 sc = scales4(W.scales, s0 + r, W.n_groups, g, lane);
+                    const f32x4 sc = PRE ? scales_f32(scl[q][r]) : scales4(W.scales, s0 + r, W.n_groups, g, lane);
 #pragma unroll
                     for (int i = 0; i < 4; i++) total[r][i] = __builtin_fmaf(sc[i], acc[r][i], total[r][i]);
                 }
@@ -361,8 +397,8 @@ __device__ __forceinline__ void chunk_mfma(const TMat& W, int s0, int c, int ks_
                 const uint4 A = a_operand<BITS>(raw[r], q), Z = make_uint4(0, 0, 0, 0);
                 const f32x4 a1 = mfma3(lo ? A : Z, B[q], f32x4{0, 0, 0, 0});
                 const f32x4 a2 = mfma3(lo ? Z : A, B[q], f32x4{0, 0, 0, 0});
-                const f32x4 s1 = scales4(W.scales, s0 + r, W.n_groups, 2 * ks, lane);
-                const f32x4 s2 = scales4(W.scales, s0 + r, W.n_groups, 2 * ks + 1, lane);
+                const f32x4 s1 = PRE ? scales_f32(scl[2 * q][r]) : scales4(W.scales, s0 + r, W.n_groups, 2 * ks, lane);
+                const f32x4 s2 = PRE ? scales_f32(scl[2 * q + 1][r]) : scales4(W.scales, s0 + r, W.n_groups, 2 * ks + 1, lane);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     total[r][i] = __builtin_fmaf(s1[i], a1[i], total[r][i]);
@@ -459,7 +495,7 @@ constexpr int ROPE_HALF_MAX = 128;
 // waiting on fin. With OUT_FLOW the outputs are written through the coherent path and the
 // workgroup then signals fout; for the residual epilogue the residual rows themselves were
 // written in the same launch, so they too are read coherently after the wait.
-template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false>
+template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false, bool PRE = false>
 __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const MMScratch& sc, const Flow& fin, const Flow& fout, int bx,
                                         int tile, uint8_t* smem) {
     constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
@@ -487,9 +523,14 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     int* tpos = reinterpret_cast<int*>(rsin + FTOK * (EPI == EPI_QKV ? a.hd / 2 : 0));  // [position][cache row] per token
     const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
 
-    // Every load of the wavefront's share is issued before any arithmetic.
+    // Every load of the wavefront's share (weights, their group scales, and the input when it
+    // was written before the launch) is issued before any arithmetic.
     uint4 raw[CPW][S];
     uint4 B[CPW * Q][3];
+    // With PRE the group scales are loaded here too (a consumer of in-launch data would otherwise
+    // load them only after its wait); launches that are short of registers leave them to the
+    // matrix loop, which the compiler schedules ahead by itself when no wait sits in between.
+    uint2 scl[PRE ? CPW : 1][PRE ? scale_slots<BITS, G16>() : 1][S];
     {
         const uint8_t* wb = W.data + (size_t(s0) * W.n_chunks * 64 + lane) * 16;
         const size_t sst = size_t(W.n_chunks) * 1024;
@@ -498,6 +539,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         for (int c = 0; c < CPW; c++) {
             if (c < nch) {
                 load_chunk<S>(wb, sst, c0 + c, raw[c]);
+                if constexpr (PRE && BITS != 16) load_scales<BITS, G16, S>(W, s0, c0 + c, (c0 + nch) * Q, scl[c]);
                 if constexpr (!IN_FLOW) {
 #pragma unroll
                     for (int q = 0; q < Q; q++) {
@@ -598,7 +640,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     for (int r = 0; r < S; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < CPW; c++)
-        if (c < nch) chunk_mfma<BITS, G16, S>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total);
+        if (c < nch) chunk_mfma<BITS, G16, S, PRE>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total, scl[PRE ? c : 0]);
     if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);  // read after the barrier below
 
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
@@ -950,7 +992,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.want = 3 * (HD / 16);
         fout.consumers = ASPLIT;
         fout.base = base + FL_Q;
-        mm_body<BITS, EPI_QKV, G16, 1, true, true>(a, pq, sc, fin, fout, r, 0, smem);
+        mm_body<BITS, EPI_QKV, G16, 1, true, true, true>(a, pq, sc, fin, fout, r, 0, smem);
         return;
     }
     r -= nq;
@@ -999,7 +1041,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fin.consumers = no;
         fin.base = base + FL_A;
         fin.mirrors = lf.m_a;
-        mm_body<BITS, EPI_RESID, G16, 1, true, true>(a, po, sc, fin, fo, r, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, 1, true, true, true>(a, po, sc, fin, fo, r, 0, smem);
         return;
     }
     r -= no;
@@ -1007,7 +1049,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         if (int(threadIdx.x) >= 64 * pg.rg * pg.kw) return;
         MMArgs a = ga;
         a.W = P.gu;
-        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true>(a, pg, sc, fo, fg, r, 0, smem);
+        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true, true>(a, pg, sc, fo, fg, r, 0, smem);
         return;
     }
     r -= ng;
@@ -1023,7 +1065,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.base = base + FL_D;
         fout.mirrors = lf.m_d;
     }
-    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true>(a, pd, sc, fg, fout, r, 0, smem);
+    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true>(a, pd, sc, fg, fout, r, 0, smem);
 }
 
 // Output head, persistent: each workgroup copies the tile's fragments (every k-step) to LDS
