@@ -77,7 +77,9 @@ constexpr unsigned FLOW_SPIN_LIMIT = 1u << 22;
 // A flow without a control block (a stage whose input was written before the launch) does not
 // wait. Every 64 polls the wait also reads the error word, so that once one wait of a launch
 // has given up, the others stop waiting at once and the launch drains.
-// Consumer `who` (0, 1, ... among the counter's consumers) polls copy who % mirrors.
+// Consumer `who` (0, 1, ... among the counter's consumers) polls copy who % mirrors. With
+// consumers > 0 the consumers count themselves and the last one puts the counter back to zero;
+// with consumers == 0 a later workgroup of the launch does that (Flow::zero0).
 __device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
     if (!fl.ctl) return;
     if (threadIdx.x == 0) {
@@ -96,13 +98,24 @@ __device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
                 break;
             __builtin_amdgcn_s_sleep(2);
         }
-        const int old = __hip_atomic_fetch_add(c0 + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == fl.consumers - 1) {
-            for (int m = 0; m < fl.mirrors; m++) __hip_atomic_store(c0 + FLOW_CNT_STRIDE * m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(c0 + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (fl.consumers > 0) {
+            const int old = __hip_atomic_fetch_add(c0 + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (old == fl.consumers - 1) {
+                for (int m = 0; m < fl.mirrors; m++) __hip_atomic_store(c0 + FLOW_CNT_STRIDE * m, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(c0 + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     __syncthreads();
+}
+
+// The counter slots a producer puts back to zero (Flow::zero0, zero1), issued with its outputs so
+// that the wait before its signal covers them too.
+__device__ __forceinline__ void flow_zero(const Flow& fl) {
+    for (int i = threadIdx.x; i < fl.nzero0; i += blockDim.x)
+        __hip_atomic_store(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.zero0 + i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = threadIdx.x; i < fl.nzero1; i += blockDim.x)
+        __hip_atomic_store(fl.ctl + FLOW_CNT0 + FLOW_CNT_STRIDE * (fl.zero1 + i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Producer r: every output store of this workgroup has completed (s_waitcnt), then its counter
@@ -110,6 +123,7 @@ __device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
 // (qkv_signal below is the producer side for q|k|v -> attention.)
 __device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
     if (!fl.ctl) return;
+    flow_zero(fl);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (int(threadIdx.x) < fl.mirrors)
@@ -121,6 +135,7 @@ __device__ __forceinline__ void flow_signal(const Flow& fl, int r) {
 // count it for every head that reads it, counter base + head (a q strip: its head; a k or v
 // strip: the heads of its group). These counters have one copy (ATTN_SPLIT consumers each).
 __device__ __forceinline__ void qkv_signal(const Flow& fl, int r, int heads, int kv_heads, int hd) {
+    flow_zero(fl);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x != 0) return;

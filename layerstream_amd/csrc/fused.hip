@@ -483,6 +483,7 @@ __device__ __forceinline__ int qkv_ref_row(int row, int hd, int qk_rows) {
 }
 
 constexpr int MAX_SPLIT = 16;
+constexpr int MAX_KW = 16;  // wavefronts along K of one row group (mm_max_waves)
 constexpr int ROPE_HALF_MAX = 128;
 
 // Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
@@ -641,27 +642,33 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
 #pragma unroll
     for (int c = 0; c < CPW; c++)
         if (c < nch) chunk_mfma<BITS, G16, S, PRE>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total, scl[PRE ? c : 0]);
-    if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);  // read after the barrier below
-
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
-    // rows 16 r + 4 (l / 16) + i of token l % 16.
+    // rows 16 r + 4 (l / 16) + i of token l % 16. Wavefront 0 works out 1 / rms (read after the
+    // barriers below) while the other wavefronts finish their products.
     if (p.kw > 1) {
         f32x4* red = reinterpret_cast<f32x4*>(smem);
 #pragma unroll
         for (int r = 0; r < S; r++) red[(wv * S + r) * 64 + lane] = total[r];
+        if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
         __syncthreads();
         for (int e = threadIdx.x; e < p.rg * S * 64; e += nthr) {
             const int g = e / (S * 64), r = (e / 64) % S, ln = e % 64;
-            f32x4 sum = red[((g * p.kw) * S + r) * 64 + ln];
-            for (int k = 1; k < p.kw; k++) {
-                const f32x4 v = red[((g * p.kw + k) * S + r) * 64 + ln];
+            // All kw reads in flight at once, then the sums in wavefront order.
+            f32x4 v[MAX_KW];
 #pragma unroll
-                for (int i = 0; i < 4; i++) sum[i] += v[i];
-            }
+            for (int k = 0; k < MAX_KW; k++)
+                if (k < p.kw) v[k] = red[((g * p.kw + k) * S + r) * 64 + ln];
+            f32x4 sum = v[0];
+#pragma unroll
+            for (int k = 1; k < MAX_KW; k++)
+                if (k < p.kw)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sum[i] += v[k][i];
 #pragma unroll
             for (int i = 0; i < 4; i++) tl[(16 * (S * g + r) + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
         }
     } else {
+        if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
 #pragma unroll
         for (int r = 0; r < S; r++)
 #pragma unroll
@@ -748,18 +755,17 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         if constexpr (OUT_FLOW) qkv_signal(fout, rb, a.heads, a.kv_heads, a.hd);
     } else if constexpr (EPI == EPI_RESID) {
         if constexpr (XCOH) {
-            // Residual rows, fragments and partials all go through the coherent path.
-            const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
+            // Residual rows, fragments and partials all go through the coherent path. The new
+            // rows stay in xr until after the barrier below: a barrier waits for the wavefront's
+            // outstanding stores, so every store of this epilogue is issued after it.
 #pragma unroll
             for (int u = 0; u < XR; u++) {
                 const int e = threadIdx.x + u * nthr, rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
-                if (e >= rows_wg * FTOK) break;
-                float xn = 0.0f;
-                if (tok < nt && row < W.rows) {
-                    xn = __fadd_rn(xr[u], tl[e]);
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xn), rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1);
+                if (e < rows_wg * FTOK) {
+                    const float xn = tok < nt && row < W.rows ? __fadd_rn(xr[u], tl[e]) : 0.0f;
+                    xr[u] = xn;
+                    tl[e] = xn;
                 }
-                tl[e] = xn;
             }
         } else {
             for (int e = threadIdx.x; e < rows_wg * FTOK; e += nthr) {
@@ -799,27 +805,41 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 else a.oss[(size_t(tile) * a.oss_slots + slot) * FTOK + tok] = v;
             }
         }
-        if constexpr (XCOH) flow_signal(fout, rb);
+        if constexpr (XCOH) {
+            const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
+#pragma unroll
+            for (int u = 0; u < XR; u++) {
+                const int e = threadIdx.x + u * nthr, rl = e / FTOK, tok = e % FTOK, row = row0 + rl;
+                if (e < rows_wg * FTOK && tok < nt && row < W.rows)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xr[u]), rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1);
+            }
+            flow_signal(fout, rb);
+        }
     } else if constexpr (EPI == EPI_SILU) {
-        // rows: [h gate rows | h up rows] for act columns h rb + [0, h), h = rows_wg / 2
+        // rows: [h gate rows | h up rows] for act columns h rb + [0, h), h = rows_wg / 2. Each
+        // thread forms one SiLU(g) * u value in place of its gate value, then the fragments.
         const int hw = rows_wg / 2;
         uint8_t* tf = a.ofrags + size_t(tile) * a.ofrag_stride;
         const __amdgpu_buffer_rsrc_t rof = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(a.ofrag_stride), BUF_DWORD3);
+        for (int e = threadIdx.x; e < hw * FTOK; e += nthr) {
+            const int tok = e % FTOK;
+            float v = 0.0f;
+            if (tok < nt) {
+                float g = tl[e], up = tl[hw * FTOK + e];
+                if (a.ss) {
+                    g = __fmul_rn(g, inv[tok]);
+                    up = __fmul_rn(up, inv[tok]);
+                }
+                v = __fmul_rn(g / (1.0f + expf(-g)), up);
+            }
+            tl[e] = v;
+        }
+        __syncthreads();
         for (int q = threadIdx.x; q < (hw / 8) * FTOK; q += nthr) {
             const int cg = q / FTOK, tok = q % FTOK, col = hw * rb + 8 * cg;
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v[j] = 0.0f;
-                if (tok < nt) {
-                    float g = tl[(8 * cg + j) * FTOK + tok], up = tl[(hw + 8 * cg + j) * FTOK + tok];
-                    if (a.ss) {
-                        g = __fmul_rn(g, inv[tok]);
-                        up = __fmul_rn(up, inv[tok]);
-                    }
-                    v[j] = __fmul_rn(g / (1.0f + expf(-g)), up);
-                }
-            }
+            for (int j = 0; j < 8; j++) v[j] = tl[(8 * cg + j) * FTOK + tok];
             if constexpr (OUT_FLOW) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
             else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
@@ -982,7 +1002,6 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         if (l > 0) {
             fin.ctl = lf.ctl;
             fin.producers = fin.per = pd.nrb;
-            fin.consumers = nq;
             fin.base = base - FLOW_LAYER_STRIDE + FL_D;
             fin.mirrors = lf.m_d;
         }
@@ -990,8 +1009,15 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.ctl = lf.ctl;
         fout.producers = nq;
         fout.want = 3 * (HD / 16);
-        fout.consumers = ASPLIT;
         fout.base = base + FL_Q;
+        if (l > 0 && r == 0) {
+            // Every workgroup of the previous layer's gate|up and down has finished waiting (the
+            // down row blocks this workgroup waited for merged every K split).
+            fout.zero0 = base - FLOW_LAYER_STRIDE + FL_O;
+            fout.nzero0 = lf.m_o;
+            fout.zero1 = base - FLOW_LAYER_STRIDE + FL_G;
+            fout.nzero1 = (pg.nrb + lf.gu_per - 1) / lf.gu_per * lf.m_g;
+        }
         mm_body<BITS, EPI_QKV, G16, 1, true, true, true>(a, pq, sc, fin, fout, r, 0, smem);
         return;
     }
@@ -1005,29 +1031,29 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fin.ctl = lf.ctl;
         fin.producers = nq;
         fin.want = 3 * (HD / 16);
-        fin.consumers = ASPLIT;
         fin.base = base + FL_Q;
         Flow fout;
         fout.ctl = lf.ctl;
         fout.producers = fout.per = aa.heads;
-        fout.consumers = no;
         fout.base = base + FL_A;
         fout.mirrors = lf.m_a;
         attn_body<HD, true, true>(A, r % ASPLIT, r / ASPLIT, 0, fout, smem, fin);
         return;
     }
     r -= na;
+    // Counters of these flows go back to zero in the next layer's first q|k|v workgroup; after the
+    // last layer there is none, so there the consumers count themselves.
     Flow fo;  // o -> gate|up
     fo.ctl = lf.ctl;
     fo.producers = fo.per = no;
-    fo.consumers = ng;
+    fo.consumers = last ? ng : 0;
     fo.base = base + FL_O;
     fo.mirrors = lf.m_o;
     Flow fg;  // gate|up -> down, one counter per down K split
     fg.ctl = lf.ctl;
     fg.producers = ng;
     fg.per = lf.gu_per;
-    fg.consumers = pd.nrb;
+    fg.consumers = last ? pd.nrb : 0;
     fg.base = base + FL_G;
     fg.mirrors = lf.m_g;
     if (r < no) {
@@ -1038,9 +1064,18 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         Flow fin;
         fin.ctl = lf.ctl;
         fin.producers = fin.per = aa.heads;
-        fin.consumers = no;
         fin.base = base + FL_A;
         fin.mirrors = lf.m_a;
+        if (r == 0) {
+            // Every attention workgroup of this layer, and so every q|k|v workgroup, has finished
+            // waiting (all heads merged).
+            fo.zero0 = base + FL_Q;
+            fo.nzero0 = aa.heads;
+            if (l > 0) {
+                fo.zero1 = base - FLOW_LAYER_STRIDE + FL_D;
+                fo.nzero1 = lf.m_d;
+            }
+        }
         mm_body<BITS, EPI_RESID, G16, 1, true, true, true>(a, po, sc, fin, fo, r, 0, smem);
         return;
     }
@@ -1049,6 +1084,11 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         if (int(threadIdx.x) >= 64 * pg.rg * pg.kw) return;
         MMArgs a = ga;
         a.W = P.gu;
+        if (r == 0) {
+            // Every o workgroup of this layer has finished waiting.
+            fg.zero0 = base + FL_A;
+            fg.nzero0 = lf.m_a;
+        }
         mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true, true>(a, pg, sc, fo, fg, r, 0, smem);
         return;
     }
@@ -1061,8 +1101,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     if (!last) {
         fout.ctl = lf.ctl;
         fout.producers = fout.per = pd.nrb;
-        fout.consumers = nq;
-        fout.base = base + FL_D;
+        fout.base = base + FL_D;  // back to zero in the next layer's first o workgroup
         fout.mirrors = lf.m_d;
     }
     mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true>(a, pd, sc, fg, fout, r, 0, smem);
@@ -1230,6 +1269,7 @@ MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
     if (p.kw > waves_k) p.kw = waves_k;
     if (p.rg > max_waves) throw std::runtime_error("too many row groups for one workgroup");
     if (p.rg * p.kw > max_waves) p.kw = max_waves / p.rg;
+    if (p.kw > MAX_KW) throw std::runtime_error("more wavefronts along K than the row-group reduction adds");
     p.nsplit = (waves_k + p.kw - 1) / p.kw;
     while (p.nsplit > MAX_SPLIT && p.rg * (p.kw + 1) <= max_waves) {
         p.kw++;

@@ -168,6 +168,10 @@ struct Flow {
     int base = 0;       // first counter slot of this launch
     int want = 0;       // when set: the count every counter waits for (producers may feed several)
     int mirrors = 1;    // copies of each counter
+    // Counter slots this producer puts back to zero just before it signals (two ranges of slots:
+    // first, count), for flows whose consumers (consumers == 0: they do not count themselves)
+    // have all finished waiting by then.
+    int zero0 = 0, nzero0 = 0, zero1 = 0, nzero1 = 0;
 };
 // Control block words: error flag, greedy acceptance (m, next), then the counter slots (gate|up
 // -> down from slot 0, FLOW_GU_MIRRORS per down K split; q|k|v -> attention one per head from
