@@ -216,14 +216,26 @@ def _short(name):
     return name.split("(")[0].replace("void ", "").strip()
 
 
+def _step_ends(names):
+    """Indices of the last kernel of each pass that ends with the head: k_head_final when the
+    pass launches it, else the head itself (a verify step whose head finishes the argmax)."""
+    ends = []
+    for i, n in enumerate(names):
+        nxt = names[i + 1] if i + 1 < len(names) else ""
+        if "k_head_final" in n or ("k_head<" in n and "k_head_final" not in nxt):
+            ends.append(i)
+    return ends
+
+
 def summarize(args):
     """Per-kernel figures over the last --last verify steps of a profiled bench run (each step
-    ends with k_head_final): durations from a --kernel-trace CSV, or counters from a --pmc CSV."""
+    ends with the head, or with k_head_final where it runs): durations from a --kernel-trace
+    CSV, or counters from a --pmc CSV."""
     if args.trace_summary:
         rows = _csv_rows(args.trace_summary)
         kn, ts, te = _col(rows[0], "Kernel_Name"), _col(rows[0], "Start_Timestamp"), _col(rows[0], "End_Timestamp")
         rows.sort(key=lambda r: int(r[ts]))
-        ends = [i for i, r in enumerate(rows) if "k_head_final" in r[kn]]
+        ends = _step_ends([r[kn] for r in rows])
         if len(ends) <= args.last:
             raise SystemExit(f"the trace holds {len(ends)} verify steps, fewer than --last {args.last} + 1")
         sel = rows[ends[-args.last - 1] + 1 : ends[-1] + 1]
@@ -244,7 +256,7 @@ def summarize(args):
             d = disp.setdefault(int(r[di]), {"name": _short(r[kn])})
             d[r[cn]] = d.get(r[cn], 0.0) + float(r[cv])
         order = sorted(disp)
-        ends = [d for d in order if "k_head_final" in disp[d]["name"]]
+        ends = [order[i] for i in _step_ends([disp[d]["name"] for d in order])]
         if len(ends) <= args.last:
             raise SystemExit(f"the counters cover {len(ends)} verify steps, fewer than --last {args.last} + 1")
         sel = [disp[d] for d in order if ends[-args.last - 1] < d <= ends[-1]]

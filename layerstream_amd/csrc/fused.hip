@@ -206,10 +206,15 @@ __device__ void row_frags(const float* xr, int i, int cols, const float* __restr
 }
 
 __global__ __launch_bounds__(256) void k_tile_embed(TMat E, const uint32_t* __restrict__ tokens, float* __restrict__ x,
-                                                    const float* __restrict__ w, uint8_t* frags, float* ss) {
+                                                    const float* __restrict__ w, uint8_t* frags, float* ss, StageMirror sm) {
     extern __shared__ float lds[];
     const int i = blockIdx.x;
-    const int r = int(tokens[i]), strip = r / 16, rl = r % 16;
+    // Host words are read at system scope (past the GPU caches, which may hold an earlier call's).
+    const int r = sm.host ? __hip_atomic_load(sm.host + sm.tok_off + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : int(tokens[i]);
+    if (sm.host && i == 0)
+        for (int k = threadIdx.x; k < sm.words; k += blockDim.x)
+            sm.dev[k] = __hip_atomic_load(sm.host + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    const int strip = r / 16, rl = r % 16;
     const int cc = tile_chunk_cols(E.bits);
     float* xr = x + size_t(i) * E.cols;
     for (int col = threadIdx.x; col < E.cols; col += blockDim.x) {
@@ -236,9 +241,11 @@ __global__ __launch_bounds__(256) void k_tile_embed(TMat E, const uint32_t* __re
 }
 
 void tile_embed(const TMat& E, const uint32_t* tokens, int n, float* x, const float* w, uint8_t* frags, float* ss,
-                hipStream_t s) {
+                hipStream_t s, const StageMirror& mirror) {
     if (E.cols % 8) throw std::runtime_error("embedding width must be a multiple of 8");
-    hipLaunchKernelGGL(k_tile_embed, dim3(n), dim3(256), size_t(E.cols) * 4, s, E, tokens, x, w, frags, ss);
+    if (mirror.host && (!mirror.dev || mirror.tok_off < 0 || mirror.tok_off + n > mirror.words))
+        throw std::runtime_error("staging mirror does not hold the tokens");
+    hipLaunchKernelGGL(k_tile_embed, dim3(n), dim3(256), size_t(E.cols) * 4, s, E, tokens, x, w, frags, ss, mirror);
     FCHECK(hipGetLastError());
 }
 
@@ -1107,6 +1114,79 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true>(a, pd, sc, fg, fout, r, 0, smem);
 }
 
+// The head's last workgroup to finish: partials were stored at agent scope and waited on before
+// the count moved, so the last one reads them all (agent-scope loads, past its own L2) and does
+// what k_head_final does for a verify block: per token the best partial (src/spec.rs:41-49; a
+// NaN logit of row 0 makes the argmax 0), then greedy acceptance (src/spec.rs:119-127). The
+// result also goes straight to pinned host memory, which saves the copy back.
+template <int WAVES>
+__device__ __forceinline__ void head_final_last(const MMArgs& a, int* lds) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int total = int(gridDim.x * gridDim.y);
+        const int old = __hip_atomic_fetch_add(a.fin_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == total - 1;
+        if (last) __hip_atomic_store(a.fin_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds[0] = last;
+    }
+    __syncthreads();
+    if (!lds[0]) return;
+    uint32_t* am = reinterpret_cast<uint32_t*>(lds + 1);  // [a.n]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nb = int(gridDim.x);
+    for (int i = w; i < a.n; i += WAVES) {
+        const size_t base = size_t(i / FTOK) * a.arg_stride * FTOK + i % FTOK;
+        float v = NAN;
+        int ix = 0x7fffffff;
+        // Four partials per lane in flight at once (one workgroup per CU: 256 blocks in one round).
+        for (int b0 = lane; b0 < nb; b0 += 4 * 64) {
+            float xv[4];
+            int xi[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int b = b0 + 64 * u;
+                const size_t at = base + size_t(b < nb ? b : 0) * FTOK;
+                xv[u] = __hip_atomic_load(a.arg_val + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                xi[u] = __hip_atomic_load(a.arg_idx + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (b0 + 64 * u < nb && beats(xv[u], xi[u], v, ix)) {
+                    v = xv[u];
+                    ix = xi[u];
+                }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o, 64);
+            const int oi = __shfl_xor(ix, o, 64);
+            if (beats(ov, oi, v, ix)) {
+                v = ov;
+                ix = oi;
+            }
+        }
+        if (lane == 0) {
+            const float r0 = __hip_atomic_load(a.row0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            am[i] = isnan(r0) ? 0u : uint32_t(ix);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < a.n; i += blockDim.x) a.fin_amax[i] = am[i];
+    if (threadIdx.x == 0) {
+        int m = 0;
+        while (m < a.n - 1 && am[m] == a.fin_block[m + 1]) m++;
+        const uint32_t next = am[m];
+        const int err = __hip_atomic_load(a.fin_ctl + FLOW_ERR, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.fin_ctl[FLOW_ACC] = m;
+        a.fin_ctl[FLOW_ACC + 1] = int(next);
+        __hip_atomic_store(a.fin_host + FLOW_ERR, uint32_t(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.fin_host + FLOW_ACC, uint32_t(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(a.fin_host + FLOW_ACC + 1, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        // Complete before the wave ends (no fence: one would write back this XCD's whole L2).
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+}
+
 // Output head, persistent: each workgroup copies the tile's fragments (every k-step) to LDS
 // once; its wavefronts then stream 64-row groups of the table over the whole K range, PF chunks
 // ahead, and reduce each group to logits and a per-token (value, index) argmax partial inside
@@ -1120,6 +1200,7 @@ template <bool G16>
 constexpr int head_waves() { return G16 ? 8 : 10; }
 constexpr int HEAD_WAVES_MAX = 10;
 constexpr int HEAD_BMAX = 16;  // fragment slots (16 B) copied to LDS per thread
+constexpr int HEAD_FIN_MAX = 128;  // tokens of a head launch that does its own final reduction
 
 template <int BITS, bool G16>
 __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n_groups) {
@@ -1202,7 +1283,10 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
                                 bix = a.row_base + row;
                             }
                         }
-                        if (row == 0 && a.row0) a.row0[ibase + tok] = v;
+                        if (row == 0 && a.row0) {
+                            if (a.fin_cnt) __hip_atomic_store(a.row0 + ibase + tok, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            else a.row0[ibase + tok] = v;
+                        }
                     }
 #pragma unroll
                 for (int o = 16; o < 64; o <<= 1) {
@@ -1240,9 +1324,15 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
                 ix = wv_i[w * FTOK + tok];
             }
         const size_t at = (size_t(tile) * a.arg_stride + a.arg_off + bx) * FTOK + tok;
-        a.arg_val[at] = v;
-        a.arg_idx[at] = ix;
+        if (a.fin_cnt) {
+            __hip_atomic_store(a.arg_val + at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.arg_idx + at, ix, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            a.arg_val[at] = v;
+            a.arg_idx[at] = ix;
+        }
     }
+    if (a.fin_cnt) head_final_last<HEAD_WAVES>(a, reinterpret_cast<int*>(wv_i + HEAD_WAVES * FTOK));
 }
 
 int device_cu_count() {
@@ -1570,11 +1660,23 @@ void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& 
 }
 
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
-    const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES_MAX * FTOK * 8;
+    if (a.fin_cnt && (a.arg_off != 0 || a.n > HEAD_FIN_MAX || !a.fin_ctl || !a.fin_block || !a.fin_amax || !a.fin_host || !a.row0))
+        throw std::runtime_error("the head's own final reduction takes one launch of at most 128 tokens and all its buffers");
+    // LDS: fragments, 1 / rms, per-wavefront partials, then the final reduction's flag and argmax.
+    const size_t lds = size_t(a.W.n_chunks) * (tile_chunk_cols(a.W.bits) / 32) * 3 * 1024 + FTOK * 4 + HEAD_WAVES_MAX * FTOK * 8 +
+                       (a.fin_cnt ? 4 * (1 + HEAD_FIN_MAX) : 0);
     const int copy_slots = a.W.n_chunks * (tile_chunk_cols(a.W.bits) / 32) * 3 * 64;  // 16-byte fragment slots of a tile
     const int min_threads = 64 * std::min(head_waves<true>(), head_waves<false>());
     if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX || copy_slots > HEAD_BMAX * min_threads) {
-        launch<EPI_HEAD, 4>(a, p, sc, s);
+        MMArgs g = a;
+        g.fin_cnt = nullptr;
+        launch<EPI_HEAD, 4>(g, p, sc, s);
+        if (a.fin_cnt) {
+            // The generic path leaves the final reduction to its own kernel and a copy.
+            head_argmax_final(a.arg_val, a.arg_idx, a.arg_stride, p.nrb, a.row0, a.n, a.fin_amax, a.fin_block,
+                              reinterpret_cast<uint32_t*>(a.fin_ctl + FLOW_ACC), s);
+            FCHECK(hipMemcpyAsync(a.fin_host, a.fin_ctl, (FLOW_ACC + 2) * 4, hipMemcpyDeviceToHost, s));
+        }
         return p.nrb;
     }
     // One workgroup per CU (the fragments fill most of its LDS).

@@ -67,10 +67,19 @@ __host__ __device__ constexpr int gu_wave_strips(int bits, int group) { return (
 // so two strips halve the input-fragment reads per weight byte.
 constexpr int DOWN_STRIPS = 2;
 
+// A call's staged words (positions, then tokens) read by the first kernel of a pass straight from
+// pinned host memory and mirrored into device memory for the later kernels, in place of a copy.
+struct StageMirror {
+    const int* host = nullptr;  // pinned host words (device-accessible)
+    int* dev = nullptr;         // their device copy
+    int words = 0;
+    int tok_off = 0;  // first token word
+};
 // Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization) into
-// x [n][cols], plus fragments of x * w and sum-of-squares partials.
+// x [n][cols], plus fragments of x * w and sum-of-squares partials. With a mirror the tokens are
+// read from its host words (tok_off on) and all its words are copied to the device.
 void tile_embed(const TMat& E, const uint32_t* tokens, int n, float* x, const float* w, uint8_t* frags, float* ss,
-                hipStream_t s);
+                hipStream_t s, const StageMirror& mirror = StageMirror{});
 // Fragments (of x * w, or of x when w is null) and sum-of-squares partials (when ss is not null)
 // of rows [0, n) of x [n][cols].
 void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, float* ss, hipStream_t s);
@@ -116,6 +125,15 @@ struct MMArgs {
     // input, so that a later launch finds them in the memory-side cache.
     const uint8_t* pf = nullptr;
     size_t pf_bytes = 0;
+    // Head only: the last workgroup to finish (fin_cnt, zero between launches, counts them)
+    // reduces every workgroup's argmax partials (row0 holds logits[.][0]) into fin_amax, applies
+    // greedy acceptance to the verify block fin_block (n tokens; src/spec.rs:119-127) and writes
+    // [ctl[FLOW_ERR], m, next] to fin_host (pinned host memory) and m, next to ctl + FLOW_ACC.
+    int* fin_cnt = nullptr;
+    int* fin_ctl = nullptr;
+    const uint32_t* fin_block = nullptr;
+    uint32_t* fin_amax = nullptr;
+    uint32_t* fin_host = nullptr;
 };
 
 // Work split of one launch: each wavefront streams s strips (16 s rows); a workgroup owns rg
@@ -173,10 +191,11 @@ struct Flow {
     // have all finished waiting by then.
     int zero0 = 0, nzero0 = 0, zero1 = 0, nzero1 = 0;
 };
-// Control block words: error flag, greedy acceptance (m, next), then the counter slots (gate|up
+// Control block words: error flag, greedy acceptance (m, next), the head's finished-workgroup
+// count (its own 128-byte line), then the counter slots (gate|up
 // -> down from slot 0, FLOW_GU_MIRRORS per down K split; q|k|v -> attention one per head from
 // slot 0; attention -> o at FLOW_ATTN_O, FLOW_AO_MIRRORS copies).
-enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 48, FLOW_ATTN_O = 40 };
+enum { FLOW_ERR = 0, FLOW_ACC = 1, FLOW_FIN = 32, FLOW_CNT0 = 64, FLOW_CNT_STRIDE = 64, FLOW_COUNTERS = 48, FLOW_ATTN_O = 40 };
 constexpr int FLOW_GU_MIRRORS = 2, FLOW_AO_MIRRORS = 8;
 constexpr int FLOW_WORDS = FLOW_CNT0 + FLOW_CNT_STRIDE * FLOW_COUNTERS;
 
@@ -254,7 +273,8 @@ void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& 
                  const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s);
 
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
-// partials at [tile][arg_off + b][16] for b below the returned count.
+// partials at [tile][arg_off + b][16] for b below the returned count. With a.fin_cnt (one head
+// launch, arg_off 0) it also does what head_argmax_final does for a verify block.
 int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
 // Final argmax over head-block partials (src/spec.rs:41-49 rule) for n tokens; row0 holds
 // logits[.][0]. With a verify block (device tokens, n of them) it also writes the greedy

@@ -185,8 +185,9 @@ public:
     void release_head_chunk(size_t) override {}
     void end_forward() override {}
     bool resident() const override { return true; }
-    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x, const float* w, uint8_t* frags, float* ss) override {
-        tile_embed(E_, dev_tokens, t, x, w, frags, ss, s_);
+    void embed(const uint32_t*, const uint32_t* dev_tokens, int t, float* x, const float* w, uint8_t* frags, float* ss,
+               const StageMirror& mirror) override {
+        tile_embed(E_, dev_tokens, t, x, w, frags, ss, s_, mirror);
     }
     ls_report report() const override {
         ls_report r{};
@@ -339,7 +340,9 @@ public:
     }
 
     bool resident() const override { return false; }
-    void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x, const float* w, uint8_t* frags, float* ss) override {
+    void embed(const uint32_t* host_tokens, const uint32_t*, int t, float* x, const float* w, uint8_t* frags, float* ss,
+               const StageMirror& mirror) override {
+        if (mirror.host) fail("a streamed table takes its tokens from the host call", LS_E_STATE);
         // Rows come from the source on every pass, as src/provider.rs:284-286.
         const size_t rb = c_.row_bytes();
         if (size_t(t) > max_rows_) fail("more embedding rows than the staging buffer holds", LS_E_STATE);
@@ -536,6 +539,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
     if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
     if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default on)
+    if (const char* e = std::getenv("LS_DIRECT")) direct_on_ = std::atoi(e) != 0;  // verify staging without copies (default on)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -740,7 +744,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     // next layer's input directly. Streamed layers: each layer's fragments are made once it has
     // arrived.
     const DevLayer* L0 = res ? &prov_->layer(0) : nullptr;
-    prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr);
+    prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr, mirror_);
     bool stacked = false;
     prof_skip_ = false;
     if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
@@ -966,6 +970,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
         const int t0 = (T - int(n_logits)) / FTOK, nh = T - FTOK * t0;
         head_off_ = size_t(T) - n_logits - size_t(FTOK) * t0;
         int blocks = 0;  // argmax partials written by this pass
+        bool fused_final = false;
         for (size_t ci = 0; ci < prov_->n_head_chunks(); ci++) {
             HeadChunk hc = prov_->head_chunk(ci);
             MMArgs a;
@@ -986,13 +991,23 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.row0 = hc.first == 0 ? row0_.as<float>() : nullptr;
             const MMPlan plan = mm_plan(hc.mat, 1, kw_head_, nh, 4);
             if (a.arg_off + plan.nrb > head_blocks_) fail("head blocks exceed the argmax buffer", LS_E_STATE);
+            if (fin_host_ && accept_block && prov_->n_head_chunks() == 1) {
+                // A verify block: the head's last workgroup finishes the argmax and the acceptance.
+                a.fin_cnt = ctl_.as<int>() + FLOW_FIN;
+                a.fin_ctl = ctl_.as<int>();
+                a.fin_block = accept_block;
+                a.fin_amax = amax_.as<uint32_t>();
+                a.fin_host = fin_host_;
+                fused_final = true;
+            }
             prof_begin();
             blocks += mm_head(a, plan, scr, s);
             prof_end(hc.mat, nh);
             prov_->release_head_chunk(ci);
         }
-        head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(),
-                          accept_block, reinterpret_cast<uint32_t*>(ctl_.as<int>() + FLOW_ACC), s);
+        if (!fused_final)
+            head_argmax_final(hpv_.as<float>(), hpi_.as<int>(), head_blocks_, blocks, row0_.as<float>(), nh, amax_.as<uint32_t>(),
+                              accept_block, reinterpret_cast<uint32_t*>(ctl_.as<int>() + FLOW_ACC), s);
 
     }
     prof_skip_ = false;
@@ -1042,11 +1057,27 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
 }
 
 void Model::verify_body(const uint32_t* block, size_t n) {
-    HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, (n + 1) * 4, hipMemcpyHostToDevice, stream_));
+    // Over resident weights the embedding kernel reads the staged words from pinned host memory
+    // (and mirrors them to the device for the later kernels) and the head writes the result back
+    // there itself: no copy either way.
+    const bool direct = direct_on_ && prov_->resident();
+    struct Reset {
+        Model* m;
+        ~Reset() {
+            m->mirror_ = StageMirror{};
+            m->fin_host_ = nullptr;
+        }
+    } reset{this};
+    if (direct) {
+        mirror_ = StageMirror{h_stage_.as<int>(), stage_.as<int>(), int(n + 1), 1};
+        fin_host_ = h_ctl_.as<uint32_t>();
+    } else {
+        HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, (n + 1) * 4, hipMemcpyHostToDevice, stream_));
+    }
     stage_pos_ = stage_.as<int>();
     const uint32_t* dtok = reinterpret_cast<const uint32_t*>(stage_.as<int>() + 1);
     forward_chunk(block, dtok, n, n, false, dtok);
-    HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, CTL_BACK * 4, hipMemcpyDeviceToHost, stream_));
+    if (!direct) HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, CTL_BACK * 4, hipMemcpyDeviceToHost, stream_));
 }
 
 // A fused launch whose wait gave up (it never does unless a producer workgroup could not run)

@@ -93,8 +93,10 @@ public:
     virtual bool resident() const = 0;
     // x[t][h] = embedding rows of host tokens (device tokens copy for the resident table); with
     // frags also the fragments of x * w and the sum-of-squares partials.
+    // With a mirror (resident tables only) the tokens are read from its pinned host words, which the
+    // kernel also copies to the device (the call's staging copy).
     virtual void embed(const uint32_t* host_tokens, const uint32_t* dev_tokens, int t, float* x, const float* w,
-                       uint8_t* frags, float* ss) = 0;
+                       uint8_t* frags, float* ss, const StageMirror& mirror) = 0;
     virtual ls_report report() const = 0;
 };
 
@@ -192,6 +194,11 @@ private:
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     int prof_ = 0;  // profiling mode (set_profiling)
+    // Verify steps over resident weights read their staged words from pinned host memory and the
+    // head writes the result there (LS_DIRECT=0: a copy each way instead).
+    bool direct_on_ = true;
+    StageMirror mirror_;
+    uint32_t* fin_host_ = nullptr;
     bool prof_skip_ = false;  // launches of this pass outside the profiled set
     bool graphs_on_ = true;
     std::map<std::pair<int, size_t>, hipGraphExec_t> graphs_;  // verify step per (sequence, block length)
