@@ -1084,7 +1084,10 @@ void Model::verify_body(const uint32_t* block, size_t n) {
 // leaves garbage behind: report it and clear the control block for the next call.
 void Model::check_flow(const int* ctl) {
     if (ctl[FLOW_ERR] == 0) return;
+    // Every counter a failed launch may have left off zero: flows, split-K, attention merges.
     HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
+    if (cnt_.p) HIPC(hipMemsetAsync(cnt_.p, 0, cnt_.n, stream_));
+    if (attn_cnt_.p) HIPC(hipMemsetAsync(attn_cnt_.p, 0, attn_cnt_.n, stream_));
     HIPC(hipStreamSynchronize(stream_));
     fail("a fused launch timed out waiting for its producers; the results of this call are invalid", LS_E_DEVICE);
 }
