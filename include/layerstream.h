@@ -170,7 +170,8 @@ typedef struct {
     uint64_t h2d_bytes;             /* bytes copied host -> device for streamed weights */
 } ls_report;
 int ls_model_report(const ls_model* m, ls_report* out);
-/* Time of the last verify step on the device (HIP events around its kernels), in ms. */
+/* Time of the last verify step in ms: host clock from its launch until its result is on the host
+ * (LS_STEP_EVENTS=1 in the environment: HIP events around its launch on the device instead). */
 double ls_model_last_step_ms(const ls_model* m);
 
 /* Profiling of the weight-streaming matvec kernels: with enable != 0, HIP events bracket each

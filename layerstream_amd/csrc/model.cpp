@@ -540,6 +540,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
     if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default on)
     if (const char* e = std::getenv("LS_DIRECT")) direct_on_ = std::atoi(e) != 0;  // verify staging without copies (default on)
+    if (const char* e = std::getenv("LS_STEP_EVENTS")) step_events_ = std::atoi(e) != 0;  // device events around each step (default off)
     x_ = DevBuf(T * h * 4);
     q_ = DevBuf(T * hq * 4);
     // Fragment buffers start at zero: padding columns are never written and must stay finite.
@@ -1103,7 +1104,8 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     // pinned buffer is free.
     h_stage_.as<int>()[0] = int(p);
     std::memcpy(h_stage_.as<int>() + 1, block, n * 4);
-    HIPC(hipEventRecord(ev0_, stream_));
+    const auto host0 = std::chrono::steady_clock::now();
+    if (step_events_) HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {
         auto it = graphs_.find(key);
         if (it == graphs_.end()) {
@@ -1128,11 +1130,12 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     } else {
         verify_body(block, n);
     }
-    HIPC(hipEventRecord(ev1_, stream_));
+    if (step_events_) HIPC(hipEventRecord(ev1_, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
     float ms = 0;
-    HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    if (step_events_) HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    else ms = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - host0).count();
     last_step_ms_ = ms;
     const int* ctl = h_ctl_.as<int>();
     pos_ = p;
@@ -1209,7 +1212,8 @@ void Model::verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint
     }
     std::memcpy(hlen + n_seq_, blocks, rows * 4);
     const size_t words = segs.size() + 3 * rows + 2 * size_t(n_seq_);
-    HIPC(hipEventRecord(ev0_, stream_));
+    const auto host0 = std::chrono::steady_clock::now();
+    if (step_events_) HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {
         const std::vector<size_t> key(lens, lens + n_seq_);
         auto it = batch_graphs_.find(key);
@@ -1234,11 +1238,12 @@ void Model::verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint
     } else {
         batch_body(blocks, rows, words, n_segs);
     }
-    HIPC(hipEventRecord(ev1_, stream_));
+    if (step_events_) HIPC(hipEventRecord(ev1_, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
     float ms = 0;
-    HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    if (step_events_) HIPC(hipEventElapsedTime(&ms, ev0_, ev1_));
+    else ms = std::chrono::duration<float, std::milli>(std::chrono::steady_clock::now() - host0).count();
     last_step_ms_ = ms;
     const uint32_t* o = h_bacc_.as<uint32_t>();
     check_flow(reinterpret_cast<const int*>(o));  // word 0 is the control block's error word

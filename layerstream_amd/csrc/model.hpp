@@ -197,6 +197,9 @@ private:
     // Verify steps over resident weights read their staged words from pinned host memory and the
     // head writes the result there (LS_DIRECT=0: a copy each way instead).
     bool direct_on_ = true;
+    // Verify steps time themselves on the host clock, from the launch until the result is back
+    // (LS_STEP_EVENTS=1: device events around the launch instead; their markers cost ~4 us a step).
+    bool step_events_ = false;
     StageMirror mirror_;
     uint32_t* fin_host_ = nullptr;
     bool prof_skip_ = false;  // launches of this pass outside the profiled set
