@@ -478,6 +478,33 @@ def test_layer_stack_and_per_layer_launches_give_identical_bits():
         assert a.pos() == b.pos()
 
 
+def test_verify_steps_without_copies_match_the_copying_path_and_the_oracle():
+    """Resident verify steps read their staged position and tokens from pinned host memory, and the
+    head's last workgroup reduces the argmax partials, applies greedy acceptance and writes
+    (error, m, next) back there (the default); LS_DIRECT=0 copies each way and runs k_head_final.
+    Same acceptance and positions either way, for blocks of one token tile and of several (the
+    last workgroup then reduces every tile's partials), two steps in a row (graph replays), each
+    checked against the oracle's greedy tokens (src/spec.rs:119-127)."""
+    m = tiny("int8")
+    g = O.plain_greedy(cpu_model(m, max_ctx=256), PROMPT, 100)
+    for n_block, m_want in [(9, 4), (9, 8), (1, 0), (17, 16), (40, 25), (40, 39)]:
+        say("verify without copies", n_block, m_want)
+        with env("LS_DIRECT", "0"):
+            a = gpu_model(m, max_ctx=256)
+        b = gpu_model(m, max_ctx=256)
+        for t in (a, b):
+            assert t.forward_argmax(PROMPT) == g[0]
+        at = 0  # g[at] is the token each step's block starts with
+        for step in range(2):
+            drafts = list(g[at + 1 : at + 1 + m_want]) + [(g[at + 1 + m_want] + 1) % T.VOCAB] * (n_block - 1 - m_want)
+            block = [g[at]] + drafts[: n_block - 1]
+            want_m = min(m_want, n_block - 1)
+            got_a, got_b = a.verify_greedy(block), b.verify_greedy(block)
+            assert got_a == got_b == (want_m, g[at + want_m + 1]), (n_block, m_want, step, got_a, got_b)
+            assert a.pos() == b.pos() == len(PROMPT) + at + want_m + 1
+            at += want_m + 1
+
+
 def test_qwen3b_int8_verify_step_matches_the_oracle():
     """The 3B shape (hidden 2048, head_dim 128, FFN 11008; the head's fragments exceed one
     workgroup's LDS, so it runs as a split-K matrix launch), int8-g64, prompt of 64 ids, one
