@@ -1202,7 +1202,10 @@ constexpr int HEAD_WAVES_MAX = 10;
 constexpr int HEAD_BMAX = 16;  // fragment slots (16 B) copied to LDS per thread
 constexpr int HEAD_FIN_MAX = 128;  // tokens of a head launch that does its own final reduction
 
-template <int BITS, bool G16>
+// CMP (one token tile of nt tokens): LDS holds only the live tokens' fragment slots, [k-step][term]
+// [column group][nt], for tables whose full fragments (16 token columns) exceed the LDS; the slots
+// are copied through registers, a few per thread at a time.
+template <int BITS, bool G16, bool CMP = false>
 __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n_groups) {
     constexpr int HEAD_WAVES = head_waves<G16>();
     extern __shared__ __align__(16) uint8_t smem[];
@@ -1215,7 +1218,8 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     const int nt = min(FTOK, a.n - tile * FTOK), ibase = tile * FTOK;
     const int nks = W.n_chunks * Q;
     uint4* bl = reinterpret_cast<uint4*>(smem);
-    float* inv = reinterpret_cast<float*>(smem + size_t(nks) * 3 * 1024);
+    const int row_slots = CMP ? 4 * nt : 64;  // LDS slots per (k-step, term)
+    float* inv = reinterpret_cast<float*>(smem + size_t(nks) * 3 * row_slots * 16);
 
     // This wavefront's groups: g = first + k * stride. Its first weight chunks go out at once.
     const int stride = gridDim.x * HEAD_WAVES, first = bx * HEAD_WAVES + wv;
@@ -1228,16 +1232,37 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
     // also covers the first HEAD_PF chunks, which the first MFMAs need anyway.
     const uint4* fb = reinterpret_cast<const uint4*>(a.frags + size_t(tile) * a.frag_stride);
     const int nb = nks * 3 * 64, nthr = 64 * HEAD_WAVES;
-    // A wavefront moves 64 slots of 16 bytes per load.
-    for (int u = 0; u < HEAD_BMAX; u++) {
-        const int w0 = wv * 64 + u * nthr;  // this wavefront's first slot; nb is a multiple of 64
-        if (w0 >= nb) break;
-        __builtin_amdgcn_global_load_lds(fb + w0 + lane, (__attribute__((address_space(3))) void*)(bl + w0), 16, 0, 0);
-    }
     uint4 raw[HEAD_PF][4];
+    if constexpr (!CMP) {
+        // A wavefront moves 64 slots of 16 bytes per load.
+        for (int u = 0; u < HEAD_BMAX; u++) {
+            const int w0 = wv * 64 + u * nthr;  // this wavefront's first slot; nb is a multiple of 64
+            if (w0 >= nb) break;
+            __builtin_amdgcn_global_load_lds(fb + w0 + lane, (__attribute__((address_space(3))) void*)(bl + w0), 16, 0, 0);
+        }
 #pragma unroll
-    for (int p = 0; p < HEAD_PF; p++)
-        if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
+        for (int p = 0; p < HEAD_PF; p++)
+            if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
+    } else {
+        // The first weight chunks go out first; then the live slots, four loads per thread in
+        // flight: LDS slot e = (row * 4 + group) * nt + token holds fragment slot row * 64 +
+        // 16 group + token.
+#pragma unroll
+        for (int p = 0; p < HEAD_PF; p++)
+            if (p < F) load_chunk<4>(wbase(p), sst, p % NC, raw[p]);
+        const int tot = nks * 3 * 4 * nt;
+        for (int e0 = threadIdx.x; e0 < tot; e0 += 4 * nthr) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int e = e0 + u * nthr, row = e / (4 * nt), rem = e % (4 * nt);
+                if (e < tot) v[u] = fb[row * 64 + 16 * (rem / nt) + rem % nt];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (e0 + u * nthr < tot) bl[e0 + u * nthr] = v[u];
+        }
+    }
     __builtin_amdgcn_s_waitcnt(0);
     if (wv == 0) {
         if (a.ss) inv_rms(a, tile, W.cols, inv);
@@ -1261,7 +1286,12 @@ __global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n
 #pragma unroll
             for (int q = 0; q < Q; q++)
 #pragma unroll
-                for (int t = 0; t < 3; t++) B[q][t] = bl[((c * Q + q) * 3 + t) * 64 + lane];
+                for (int t = 0; t < 3; t++) {
+                    if constexpr (CMP)
+                        B[q][t] = (lane & 15) < nt ? bl[(((c * Q + q) * 3 + t) * 4 + (lane >> 4)) * nt + (lane & 15)] : make_uint4(0, 0, 0, 0);
+                    else
+                        B[q][t] = bl[((c * Q + q) * 3 + t) * 64 + lane];
+                }
             chunk_mfma<BITS, G16, 4>(W, 4 * g, c, 0, nks, B, raw[p], acc, total);
             if (f + HEAD_PF < F) load_chunk<4>(wbase(f + HEAD_PF), sst, (f + HEAD_PF) % NC, raw[p]);
             if (c == NC - 1) {
@@ -1667,7 +1697,11 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
                        (a.fin_cnt ? 4 * (1 + HEAD_FIN_MAX) : 0);
     const int copy_slots = a.W.n_chunks * (tile_chunk_cols(a.W.bits) / 32) * 3 * 64;  // 16-byte fragment slots of a tile
     const int min_threads = 64 * std::min(head_waves<true>(), head_waves<false>());
-    if (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX || copy_slots > HEAD_BMAX * min_threads) {
+    // One tile whose full fragments do not fit: the live tokens' slots only.
+    const size_t lds_cmp = lds - size_t(copy_slots) * 16 + size_t(copy_slots / 64) * 4 * std::min(a.n, FTOK) * 16;
+    const bool cmp = p.rg == 1 && p.s == 4 && p.tiles == 1 && (lds > HEAD_LDS_MAX || copy_slots > HEAD_BMAX * min_threads) &&
+                     lds_cmp <= HEAD_LDS_MAX;
+    if (!cmp && (p.rg != 1 || p.s != 4 || lds > HEAD_LDS_MAX || copy_slots > HEAD_BMAX * min_threads)) {
         MMArgs g = a;
         g.fin_cnt = nullptr;
         launch<EPI_HEAD, 4>(g, p, sc, s);
@@ -1685,6 +1719,21 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
     const int waves = g16 ? head_waves<true>() : head_waves<false>();
     const int blocks = std::min(device_cu_count(), (n_groups + waves - 1) / waves);
     const dim3 grid(blocks, p.tiles), block(64 * waves);
+    if (cmp) {
+        switch (a.W.bits) {
+            case 16: go(k_head<16, false, true>, grid, block, lds_cmp, s, a, n_groups); break;
+            case 8:
+                if (g16) go(k_head<8, true, true>, grid, block, lds_cmp, s, a, n_groups);
+                else go(k_head<8, false, true>, grid, block, lds_cmp, s, a, n_groups);
+                break;
+            default:
+                if (g16) go(k_head<4, true, true>, grid, block, lds_cmp, s, a, n_groups);
+                else go(k_head<4, false, true>, grid, block, lds_cmp, s, a, n_groups);
+                break;
+        }
+        FCHECK(hipGetLastError());
+        return blocks;
+    }
     switch (a.W.bits) {
         case 16: go(k_head<16, false>, grid, block, lds, s, a, n_groups); break;
         case 8:
