@@ -126,9 +126,11 @@ def split_parts(img, cfg):
     return T.split_lsq(img.tobytes(), {"layers": cfg["layers"]})
 
 
-def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_m):
+def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_m, gpu_tokens):
     """The oracle (C restatement of the reference CPU path) on the host's cores: the same prompt
-    prefilled, then n_steps verify passes with the same drafts. Returns the JSON object."""
+    prefilled, then n_steps verify passes with the same drafts. Returns the JSON object, with the
+    oracle's accepted counts and emitted tokens compared to the GPU run's (a parity check of the
+    benchmark's own run)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_py as O
     import layerstream_amd as LS
@@ -140,7 +142,7 @@ def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_
     t0 = time.time()
     a = int(np.argmax(om.forward(prompt)))
     t_prefill = time.time() - t0
-    n_out, toks, ms_list, ms_acc = 1, 0, [], []
+    n_out, toks, ms_list, ms_acc, emitted = 1, 0, [], [], [a]
     for _ in range(n_steps):
         drafts = [d.token(n_out + i) for i in range(k)]
         block = [a] + drafts
@@ -155,6 +157,7 @@ def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_
         ms_list.append(time.perf_counter() - t1)
         ms_acc.append(m)
         a = int(am[m])
+        emitted += [int(x) for x in drafts[:m]] + [a]
         n_out += m + 1
         toks += m + 1
     d.close()
@@ -175,6 +178,8 @@ def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_
         f"C restatement of the reference CPU path (Rust toolchain unavailable), -O3 -ffp-contract=off, {cores} threads; {cpu_model}",
         "verify_ms_p50": float(np.median(ms_list) * 1e3),
         "accepted_match_gpu": ms_acc == list(gpu_m[: len(ms_acc)]),
+        "tokens_match_gpu": emitted == list(gpu_tokens[: len(emitted)]),
+        "tokens_compared": len(emitted),
     }
 
 
@@ -429,7 +434,7 @@ def run_single(args, conf):
         "acceptance": round(float(np.sum(tm)) / (K * k), 4),
         "step_algorithmic_bytes": int(sb),
         "step_hbm_frac": round(sb / (step_ms_p50 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-        "tokens_match_greedy": bool(match),
+        "spec_matches_gpu_greedy": bool(match),
         "roofline": roofline,
         "cpu_baseline": None,
     }
@@ -444,7 +449,7 @@ def run_single(args, conf):
     if not args.no_cpu:
         t0 = time.time()
         cparts = parts if img is None else split_parts(img, cfg)
-        res["cpu_baseline"] = cpu_baseline(cparts, cfg, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m))
+        res["cpu_baseline"] = cpu_baseline(cparts, cfg, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m), out_tokens)
         log(f"cpu baseline {time.time() - t0:.1f}s")
     run.close()
     drafter.close()
@@ -570,7 +575,7 @@ def run_batch(args, conf):
         "step_hbm_frac": round(sb / (p50 * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         "step_tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
         "step_mfma_frac_bf16_dense": round(flops / (p50 * 1e-3) / 2.5e15, 4),
-        "tokens_match_greedy": match,
+        "spec_matches_gpu_greedy": match,
         "roofline": roofline_of(prof, f"matrix launches (MFMA weight streaming): k_mm q|k|v, o, gate|up, down, k_head; "
                                 f"{FMT_NAME[conf['fmt'][0]]}, t={t}", traffic_path),
         "cpu_baseline": None,
@@ -580,9 +585,11 @@ def run_batch(args, conf):
         # its single-sequence rate. Timed on sequence 0's prompt and drafts.
         t0 = time.time()
         cparts = parts if img is None else split_parts(img, cfg)
-        cb = cpu_baseline(cparts, cfg, prompts[0], greedy[0], args.p_accept, 2024, k, args.cpu_steps, [])
+        cb = cpu_baseline(cparts, cfg, prompts[0], greedy[0], args.p_accept, 2024, k, args.cpu_steps, [], [])
         cb["sample"] = "sequence 0 only (the reference runs sequences one after another); " + cb["sample"]
         cb.pop("accepted_match_gpu", None)
+        cb.pop("tokens_match_gpu", None)
+        cb.pop("tokens_compared", None)
         res["cpu_baseline"] = cb
         log(f"cpu baseline {time.time() - t0:.1f}s")
     for d in drafters:

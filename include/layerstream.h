@@ -196,6 +196,14 @@ int ls_model_profile_read(ls_model* m, ls_kernel_stat* out);
  * the step launch by launch. */
 int ls_model_use_graphs(ls_model* m, int enable);
 
+/* Test hook for the error path of the in-launch waits (no counterpart in the reference). The next
+ * device pass of this model (forward, forward_multi, verify_greedy or a batched verify) starts
+ * with the control block's error word set, as if a bounded wait had given up: every wait of the
+ * pass stops waiting at once, every kernel still runs to its end, and the call returns
+ * LS_E_DEVICE with the positions unchanged. The control block is cleared afterwards, so the
+ * following call runs normally. */
+int ls_model_debug_fail_next(ls_model* m);
+
 /* ---------------------------------------------------------------------------------------
  * Speculative decoding: speculative_greedy (src/spec.rs:57-152).
  * ------------------------------------------------------------------------------------- */

@@ -148,6 +148,7 @@ SIGNATURES = {
     "ls_model_profile": (C.c_int, [P, C.c_int]),
     "ls_model_profile_read": (C.c_int, [P, C.POINTER(KernelStat)]),
     "ls_model_use_graphs": (C.c_int, [P, C.c_int]),
+    "ls_model_debug_fail_next": (C.c_int, [P]),
     "ls_matmul": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
 }
 
@@ -427,6 +428,11 @@ class Model:
     def use_graphs(self, enable: bool):
         """Replay verify steps from captured HIP graphs (default on; resident weights only)."""
         _check(lib().ls_model_use_graphs(self.h, int(enable)))
+
+    def debug_fail_next(self):
+        """Test hook: the next device pass starts with its error word set and fails with
+        LS_E_DEVICE (every in-launch wait gives up at once); positions stay unchanged."""
+        _check(lib().ls_model_debug_fail_next(self.h))
 
     @property
     def n_seq(self) -> int:

@@ -397,6 +397,13 @@ int ls_model_use_graphs(ls_model* m, int enable) {
     });
 }
 
+int ls_model_debug_fail_next(ls_model* m) {
+    return guard([&] {
+        need(m, "model");
+        m->m->debug_fail_next();
+    });
+}
+
 int ls_model_profile_read(ls_model* m, ls_kernel_stat* out) {
     return guard([&] {
         need(m, "model");

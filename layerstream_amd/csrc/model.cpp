@@ -1019,6 +1019,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
 void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax) {
     HIPC(hipSetDevice(device_));
     check_request(tok, n);
+    const size_t p0 = pos_;
+    arm_failure();
     const uint32_t* dtok = stage_tokens(tok, n);
     const size_t n_chunks = (n + PREFILL_CHUNK - 1) / PREFILL_CHUNK;
     for (size_t ci = 0; ci < n_chunks; ci++) {
@@ -1033,6 +1035,7 @@ void Model::forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argm
     HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
+    if (h_ctl_.as<int>()[FLOW_ERR]) pos_ = p0;  // a failed pass caches nothing
     check_flow(h_ctl_.as<int>());
     if (argmax) *argmax = h_out_.as<uint32_t>()[0];
 }
@@ -1044,6 +1047,8 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
         fail("asked for logits at " + std::to_string(n_logits) + " positions of " + std::to_string(n) + " tokens");
     if (n > PREFILL_CHUNK) fail("forward_multi takes at most 128 tokens at a time");
     chunk_index_ = 0;
+    const size_t p0 = pos_;
+    arm_failure();
     forward_chunk(tok, stage_tokens(tok, n), n, n_logits, logits != nullptr);
     if (logits)
         HIPC(hipMemcpy2DAsync(logits, cfg_.vocab * 4, logits_.as<float>() + head_off_ * vpad_, vpad_ * 4, cfg_.vocab * 4,
@@ -1053,6 +1058,7 @@ void Model::forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float*
     HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
     harvest();
+    if (h_ctl_.as<int>()[FLOW_ERR]) pos_ = p0;  // a failed pass caches nothing
     check_flow(h_ctl_.as<int>());
     if (argmax) std::memcpy(argmax, h_out_.p, n_logits * 4);
 }
@@ -1081,6 +1087,12 @@ void Model::verify_body(const uint32_t* block, size_t n) {
     if (!direct) HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, CTL_BACK * 4, hipMemcpyDeviceToHost, stream_));
 }
 
+void Model::arm_failure() {
+    if (!fail_next_) return;
+    fail_next_ = false;
+    HIPC(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(ctl_.as<int>() + FLOW_ERR), 1, 1, stream_));
+}
+
 // A fused launch whose wait gave up (it never does unless a producer workgroup could not run)
 // leaves garbage behind: report it and clear the control block for the next call.
 void Model::check_flow(const int* ctl) {
@@ -1104,6 +1116,7 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     // pinned buffer is free.
     h_stage_.as<int>()[0] = int(p);
     std::memcpy(h_stage_.as<int>() + 1, block, n * 4);
+    arm_failure();
     const auto host0 = std::chrono::steady_clock::now();
     if (step_events_) HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {
@@ -1212,6 +1225,7 @@ void Model::verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint
     }
     std::memcpy(hlen + n_seq_, blocks, rows * 4);
     const size_t words = segs.size() + 3 * rows + 2 * size_t(n_seq_);
+    arm_failure();
     const auto host0 = std::chrono::steady_clock::now();
     if (step_events_) HIPC(hipEventRecord(ev0_, stream_));
     if (graphs_on_ && !prof_ && prov_->resident()) {

@@ -140,6 +140,8 @@ public:
     void set_profiling(int mode);
     void set_graphs(bool on);
     ls_kernel_stat read_profile();
+    // Test hook: the next device pass starts with the control block's error word set.
+    void debug_fail_next() { fail_next_ = true; }
 
 private:
     void check_request(const uint32_t* tok, size_t n) const;
@@ -162,6 +164,8 @@ private:
     void prof_begin();
     void prof_end(const TMat& W, int nt, bool launch = true, double extra_bytes = 0);
     void check_flow(const int* ctl);
+    // Sets the error word on the stream when debug_fail_next() asked for it (outside any graph).
+    void arm_failure();
 
     Config cfg_;
     int device_;
@@ -204,6 +208,7 @@ private:
     uint32_t* fin_host_ = nullptr;
     bool prof_skip_ = false;  // launches of this pass outside the profiled set
     bool graphs_on_ = true;
+    bool fail_next_ = false;
     std::map<std::pair<int, size_t>, hipGraphExec_t> graphs_;  // verify step per (sequence, block length)
     std::map<std::vector<size_t>, hipGraphExec_t> batch_graphs_;  // batched verify step per block lengths
     std::vector<hipEvent_t> prof_ev_;

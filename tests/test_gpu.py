@@ -506,9 +506,10 @@ def test_verify_steps_without_copies_match_the_copying_path_and_the_oracle():
 
 
 def test_qwen3b_int8_verify_step_matches_the_oracle():
-    """The 3B shape (hidden 2048, head_dim 128, FFN 11008; the head's fragments exceed one
-    workgroup's LDS, so it runs as a split-K matrix launch), int8-g64, prompt of 64 ids, one
-    verify step of k=8."""
+    """The 3B shape (hidden 2048, head_dim 128, FFN 11008; the fragments of all 16 token columns
+    exceed one workgroup's LDS, so the head keeps only the live tokens' slots there and does its
+    own final reduction), int8-g64, prompt of 64 ids, one verify step of k=8. The same path over
+    a 1024-token prompt and three steps of different lengths: test_gpu_workloads.py."""
     say("3B int8: build")
     m = qwen3b((8, 64))
     rng = np.random.default_rng(3)
