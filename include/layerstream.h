@@ -269,6 +269,18 @@ int ls_greedy_generate(ls_model* m, const uint32_t* prompt, size_t n_prompt, siz
 int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const float* x_dev, size_t t,
               float* y_dev, void* stream);
 
+/* ls_matmul without any device allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and the same result bit for bit, but asynchronous: it enqueues its
+ * kernels on `stream` and returns; synchronize the stream before reading y_dev. Everything
+ * ls_matmul allocates per call (the tile-layout copy of the weights, the input fragments, the
+ * split-K pieces and counters) sits in one static device array of 32 MiB per GPU, held until the
+ * process ends; a call that needs more (for example a wide matrix in int8 above about 30 M
+ * weights) returns LS_E_INVALID. Calls on one GPU share that array: calls that overlap in time on
+ * one GPU (other streams, other threads) race and must be ordered by the caller. */
+int ls_matmul_noalloc(ls_format f, const void* w_dev, size_t rows, size_t cols, const float* x_dev, size_t t,
+                      float* y_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -150,6 +150,7 @@ SIGNATURES = {
     "ls_model_use_graphs": (C.c_int, [P, C.c_int]),
     "ls_model_debug_fail_next": (C.c_int, [P]),
     "ls_matmul": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
+    "ls_matmul_noalloc": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
 }
 
 _lib = None

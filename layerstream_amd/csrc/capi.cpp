@@ -6,6 +6,7 @@
 
 #include "model.hpp"
 #include "spec.hpp"
+#include "static_mm.hpp"
 
 struct ls_source {
     std::unique_ptr<ls::Source> s;
@@ -460,6 +461,21 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
         a.ldo = int(rows);
         ls::mm_residual(a, plan, ls::MMScratch{part.as<float>(), cnt.as<int>()}, s);
         HIPC(hipStreamSynchronize(s));
+    });
+}
+
+int ls_matmul_noalloc(ls_format f, const void* w_dev, size_t rows, size_t cols, const float* x_dev, size_t t, float* y_dev,
+                      void* stream) {
+    return guard([&] {
+        need(w_dev, "weights");
+        need(x_dev, "input");
+        need(y_dev, "output");
+        ls::Format F = ls::Format::from(f);
+        F.validate({cols});
+        if (t == 0 || t > 128) ls::fail("t must be between 1 and 128");
+        if (rows == 0 || rows > (1u << 24) || cols > (1u << 24)) ls::fail("matrix shape out of range");
+        ls::matmul_static(F.bits, F.group, static_cast<const uint8_t*>(w_dev), int(rows), int(cols), x_dev, int(t), y_dev,
+                          static_cast<hipStream_t>(stream));
     });
 }
 
