@@ -294,6 +294,9 @@ def main():
     ap.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel-trace CSV of a bench run and exit")
     ap.add_argument("--pmc-summary", metavar="CSV", help="summarise a rocprofv3 counter-collection CSV of a bench run and exit")
     ap.add_argument("--last", type=int, default=ROOF_STEPS, help="verify steps the summaries cover (the last ones of the run)")
+    ap.add_argument("--stage-timeline", action="store_true",
+                    help="run the workload through the persistent layer pass (LS_PASS=1) with its per-unit timeline and print a "
+                    "per-stage summary of the last verify step instead of the JSON line")
     args = ap.parse_args()
     if args.trace_summary or args.pmc_summary:
         summarize(args)
@@ -315,6 +318,11 @@ def main():
         conf["prompt"] = args.ctx
     if not args.cpu_steps:
         args.cpu_steps = 8 if conf["model"] == "3b" else 24
+    if args.stage_timeline:
+        if conf["batch"] > 1:
+            sys.exit("--stage-timeline takes a single-sequence workload")
+        os.environ["LS_PASS"] = "1"
+        os.environ["LS_PASS_TIMELINE"] = "1"
     if conf["batch"] > 1:
         run_batch(args, conf)
     else:
@@ -377,6 +385,14 @@ def run_single(args, conf):
     hip_sync()
     wall = time.perf_counter() - t0
     rep1 = model.report()
+    if args.stage_timeline:
+        tl = model.debug_timeline()
+        if tl is None:
+            sys.exit("the persistent layer pass does not fit this model")
+        print_stage_timeline(tl, conf, args, wall / K)
+        run.close()
+        drafter.close()
+        return
     # Per-launch timing of the matrix kernels: HIP events on the compute stream around every
     # launch, over ROOF_STEPS further verify steps of the same run (kept out of the timed steps,
     # whose launches they would space out).
@@ -454,6 +470,54 @@ def run_single(args, conf):
     run.close()
     drafter.close()
     print(json.dumps(res), flush=True)
+
+
+STAGES = ["q|k|v", "attention", "o", "gate|up", "down"]
+
+
+def print_stage_timeline(tl, conf, args, step_s):
+    """Per-stage summary of the persistent pass's stamps for the last verify step (100 MHz ticks,
+    [workgroup][layer][stage][32]: 0 start, 1 + w wavefront w's input, 9 1/rms, 10 products summed,
+    11 stores issued, 12 done, 13 flags seen, 16 + w wavefront w's products, 24 flag store
+    acknowledged). Layers 1 .. L-2 (the first reads its input from before the launch, the last
+    writes the head's layouts)."""
+    tl = tl.astype(np.int64)
+    L = tl.shape[1]
+    first = tl[:, :, :, 0][tl[:, :, :, 0] > 0].min()
+    t = np.where(tl > 0, (tl - first) / 100.0, np.nan)  # microseconds from the first start
+    span = np.nanmax(t[:, :, :, 12])
+    mid = range(1, L - 1)
+
+    def last(a):
+        return float(np.nanmax(a)) if not np.all(np.isnan(a)) else float("nan")
+
+    print(f"# Persistent layer pass, per-stage timeline ({args.config}: {describe(conf)}, k={conf['k']})\n")
+    print(f"Verify step {step_s * 1e3:.3f} ms on the host clock (timeline stamps on: each unit also waits for its flag's "
+          f"store); pass {span:.1f} us, {span / L:.2f} us per layer; units per stage "
+          f"{[int((tl[:, 1, s, 0] > 0).sum()) for s in range(5)]}.\n")
+    print("Critical path per stage, us after the previous stage's last flag was acknowledged (mean over layers 1..L-2):\n")
+    print("| stage | last flags seen | last input | last 1/rms | last products summed | last stores issued | last flag acknowledged |")
+    print("|---|---|---|---|---|---|---|")
+    for s in range(5):
+        rows = []
+        for l in mid:
+            prev = last(t[:, l - 1, 4, 24]) if s == 0 else last(t[:, l, s - 1, 24])
+            v = t[:, l, s]
+            rows.append([last(v[:, 13]) - prev, last(v[:, 1:9]) - prev, last(v[:, 9]) - prev, last(v[:, 10]) - prev,
+                         last(v[:, 11]) - prev, last(v[:, 24]) - prev])
+        r = np.nanmean(np.array(rows, dtype=float), axis=0)
+        print("| " + STAGES[s] + " | " + " | ".join("-" if np.isnan(x) else f"{x:.2f}" for x in r) + " |")
+    print("\nPer unit, us (mean over units and layers 1..L-2):\n")
+    print("| stage | start to flags seen | flags to input (wavefront 0) | input to products (last wavefront) | products to summed | "
+          "summed to stores issued | stores to flag acknowledged |")
+    print("|---|---|---|---|---|---|---|")
+    for s in range(5):
+        v = t[:, 1 : L - 1, s].reshape(-1, tl.shape[3])
+        v = v[~np.isnan(v[:, 0])]
+        mf = np.nanmax(v[:, 16:24], axis=1) if not np.all(np.isnan(v[:, 16:24])) else np.full(len(v), np.nan)
+        win = np.nanmax(v[:, 1:9], axis=1)
+        cols = [v[:, 13] - v[:, 0], v[:, 1] - v[:, 13], mf - win, v[:, 10] - mf, v[:, 11] - v[:, 10], v[:, 24] - v[:, 11]]
+        print("| " + STAGES[s] + " | " + " | ".join("-" if np.all(np.isnan(c)) else f"{np.nanmean(c):.2f}" for c in cols) + " |")
 
 
 def run_batch(args, conf):

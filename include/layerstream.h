@@ -204,6 +204,20 @@ int ls_model_use_graphs(ls_model* m, int enable);
  * following call runs normally. */
 int ls_model_debug_fail_next(ls_model* m);
 
+/* Measurement hook (no counterpart in the reference): with LS_PASS=1 and LS_PASS_TIMELINE=1 in the
+ * environment when the model was created, every unit of the persistent layer pass records device
+ * timestamps (100 MHz s_memrealtime) per (workgroup, layer, stage): word 0 start, 1 + w wavefront
+ * w's input ready, 9 1/rms known, 10 products summed, 11 stores issued, 12 done, 13 producers'
+ * flags seen, 14 and 15 stale re-fetch counts, 16 + w wavefront w's products done, 24 the flag's
+ * store acknowledged (a timeline makes each unit wait for it). Copies up to cap words of the last
+ * pass's stamps to out (NULL: none) and returns the number of words, [workgroup][layer][5
+ * stages][32]; 0 when there is no timeline. */
+size_t ls_model_debug_timeline(ls_model* m, uint64_t* out, size_t cap);
+/* Debugging hook: a copy of one of the model's device buffers by name ("x", "xf", "ss", "q",
+ * "af", "actf", "kcache", "vcache", "pass_area"), up to cap bytes (out may be NULL). Returns the
+ * buffer's size in bytes, 0 on error. */
+size_t ls_model_debug_read(ls_model* m, const char* name, void* out, size_t cap);
+
 /* ---------------------------------------------------------------------------------------
  * Speculative decoding: speculative_greedy (src/spec.rs:57-152).
  * ------------------------------------------------------------------------------------- */

@@ -149,6 +149,8 @@ SIGNATURES = {
     "ls_model_profile_read": (C.c_int, [P, C.POINTER(KernelStat)]),
     "ls_model_use_graphs": (C.c_int, [P, C.c_int]),
     "ls_model_debug_fail_next": (C.c_int, [P]),
+    "ls_model_debug_timeline": (SZ, [P, C.POINTER(C.c_uint64), SZ]),
+    "ls_model_debug_read": (SZ, [P, C.c_char_p, P, SZ]),
     "ls_matmul": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
     "ls_matmul_noalloc": (C.c_int, [Format, P, SZ, SZ, P, SZ, P, P]),
 }
@@ -429,6 +431,29 @@ class Model:
     def use_graphs(self, enable: bool):
         """Replay verify steps from captured HIP graphs (default on; resident weights only)."""
         _check(lib().ls_model_use_graphs(self.h, int(enable)))
+
+    def debug_timeline(self) -> np.ndarray:
+        """Per-unit stamps of the last persistent pass (LS_PASS_TIMELINE=1 at creation), or None:
+        [workgroup][layer][stage (qkv, attention, o, gate|up, down)][32] in 100 MHz ticks:
+        0 start, 1 + w wavefront w's input ready, 9 1/rms known, 10 products summed, 11 stores
+        issued, 12 done, 13 flags seen, 14/15 stale re-fetches (counts), 16 + w wavefront w's
+        products done, 24 flag store acknowledged; 0 where a unit did not run or reach a stamp."""
+        n = lib().ls_model_debug_timeline(self.h, None, 0)
+        if n == 0:
+            return None
+        out = np.zeros(n, np.uint64)
+        lib().ls_model_debug_timeline(self.h, out.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+        L = self.cfg()["layers"]
+        return out.reshape(-1, L, 5, 32)
+
+    def debug_read(self, name: str) -> np.ndarray:
+        """A copy of an internal device buffer (debugging) as bytes."""
+        n = lib().ls_model_debug_read(self.h, name.encode(), None, 0)
+        if n == 0:
+            raise LayerstreamError(-1, lib().ls_last_error().decode())
+        out = np.zeros(n, np.uint8)
+        lib().ls_model_debug_read(self.h, name.encode(), out.ctypes.data, n)
+        return out
 
     def debug_fail_next(self):
         """Test hook: the next device pass starts with its error word set and fails with

@@ -18,9 +18,12 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
-# Device code: no packed-FP32 instructions (v_pk_*_f32); contraction to FMA is allowed there.
+# Device code: no packed-FP32 instructions (v_pk_*_f32), and no implicit contraction of a multiply and
+# an add into one FMA (clang's __fmul_rn / __fadd_rn are plain operators, so contraction would depend
+# on how each kernel's code was inlined and scheduled; explicit fmaf stays an FMA). Every kernel that
+# computes a value then rounds it the same way, as the reference does (Rust never fuses).
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-munsafe-fp-atomics",
-          "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
+          "-mllvm", "-amdgpu-atomic-optimizer-strategy=None", "-ffp-contract=off"]
 
 
 def _sources():

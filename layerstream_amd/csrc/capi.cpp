@@ -405,6 +405,24 @@ int ls_model_debug_fail_next(ls_model* m) {
     });
 }
 
+size_t ls_model_debug_timeline(ls_model* m, uint64_t* out, size_t cap) {
+    size_t n = 0;
+    guard([&] {
+        need(m, "model");
+        n = m->m->debug_timeline(out, cap);
+    });
+    return n;
+}
+
+size_t ls_model_debug_read(ls_model* m, const char* name, void* out, size_t cap) {
+    size_t n = 0;
+    guard([&] {
+        need(m, "model");
+        n = m->m->debug_read(name, out, cap);
+    });
+    return n;
+}
+
 int ls_model_profile_read(ls_model* m, ls_kernel_stat* out) {
     return guard([&] {
         need(m, "model");

@@ -74,6 +74,8 @@ struct StageMirror {
     int* dev = nullptr;         // their device copy
     int words = 0;
     int tok_off = 0;  // first token word
+    // When set, the embedding kernel adds one to this device word (the persistent pass's epoch).
+    int* epoch = nullptr;
 };
 // Embedding rows of tokens from a tile-layout table (src/kernels.rs:95-121 dequantization) into
 // x [n][cols], plus fragments of x * w and sum-of-squares partials. With a mirror the tokens are

@@ -607,6 +607,29 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         }
         layer_ptrs_ = DevBuf(lp.size() * sizeof(LayerPtrs));
         HIPC(hipMemcpyAsync(layer_ptrs_.p, lp.data(), layer_ptrs_.n, hipMemcpyHostToDevice, stream_));
+        // The persistent pass, when its plans fit (the plans of a one-tile pass do not depend on
+        // its token count).
+        const DevLayer& L0 = prov_->layer(0);
+        const MMPlan pq = mm_plan(L0.qkv, 1, kw_qkv_, 1, 1), po = mm_plan(L0.o, 1, kw_o_, 1, 1);
+        const MMPlan pg = gu_plan(L0.gu, kw_gu_, 1), pd = mm_plan(L0.down, 1, kw_down_, 1, DOWN_STRIPS);
+        if (const char* e = std::getenv("LS_PASS")) pass_on_ = std::atoi(e) != 0;  // persistent pass (default off)
+        if (pass_on_ && !layer_pass_unfit(1, int(c.heads), int(c.kv_heads), int(c.head_dim), pq, po, pg, pd) && c.layers < 64) {
+            int repl = 1;  // copies of the exchange buffers that many units read at once (LS_PASS_COPIES)
+            if (const char* e = std::getenv("LS_PASS_COPIES")) repl = std::atoi(e);
+            pass_shape_ = pass_area_shape(int(c.hidden), int(c.heads), int(c.kv_heads), int(c.head_dim), int(c.inter), pd, repl);
+            pass_area_ = DevBuf(2 * pass_shape_.set_bytes);
+            pass_flags_ = DevBuf(pass_shape_.flag_bytes);
+            epoch_ = DevBuf(256);
+            HIPC(hipMemsetAsync(pass_area_.p, 0, pass_area_.n, stream_));
+            HIPC(hipMemsetAsync(pass_flags_.p, 0, pass_flags_.n, stream_));
+            HIPC(hipMemsetAsync(epoch_.p, 0, epoch_.n, stream_));
+            if (const char* e = std::getenv("LS_PASS_TIMELINE"); e && std::atoi(e) != 0) {
+                pass_tl_ = DevBuf(pass_timeline_words(int(c.layers)) * 8);
+                HIPC(hipMemsetAsync(pass_tl_.p, 0, pass_tl_.n, stream_));
+            }
+        } else {
+            pass_on_ = false;
+        }
     }
     HIPC(hipStreamSynchronize(stream_));
 }
@@ -745,7 +768,11 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     // next layer's input directly. Streamed layers: each layer's fragments are made once it has
     // arrived.
     const DevLayer* L0 = res ? &prov_->layer(0) : nullptr;
-    prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr, mirror_);
+    // A one-tile pass over resident layers runs as the persistent pass (its epoch moves first).
+    const bool use_pass = res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p && pass_on_ && T <= int(FTOK);
+    StageMirror em = mirror_;
+    if (use_pass) em.epoch = epoch_.as<int>();
+    prov_->embed(tok, dtok, T, x, L0 ? L0->in_norm : nullptr, L0 ? xf : nullptr, L0 ? ss : nullptr, em);
     bool stacked = false;
     prof_skip_ = false;
     if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
@@ -803,8 +830,14 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             da.oss = ss;
             da.oss_slots = slots_h_;
             prof_begin();
-            layer_stack(layer_ptrs_.as<LayerPtrs>(), int(c.layers), size_t(cur_) * max_ctx_ * kv, qa, pq, attn_scratch_.as<float>(),
-                        attn_cnt_.as<int>(), af_.as<uint8_t>(), oa, po, ga, pg, da, pd, scr, ctl_.as<int>(), s);
+            if (use_pass) {
+                const PassArea area = pass_area_bind(pass_shape_, pass_area_.as<uint8_t>(), pass_flags_.as<int>());
+                layer_pass(layer_ptrs_.as<LayerPtrs>(), int(c.layers), size_t(cur_) * max_ctx_ * kv, qa, pq, oa, po, ga, pg, da, pd, area,
+                           ctl_.as<int>(), epoch_.as<int>(), pass_tl_.p ? pass_tl_.as<uint64_t>() : nullptr, s);
+            } else {
+                layer_stack(layer_ptrs_.as<LayerPtrs>(), int(c.layers), size_t(cur_) * max_ctx_ * kv, qa, pq, attn_scratch_.as<float>(),
+                            attn_cnt_.as<int>(), af_.as<uint8_t>(), oa, po, ga, pg, da, pd, scr, ctl_.as<int>(), s);
+            }
             for (size_t l = 0; l < c.layers; l++) {
                 const DevLayer& L = prov_->layer(l);
                 prof_end(L.qkv, T, l == 0);
@@ -1085,6 +1118,24 @@ void Model::verify_body(const uint32_t* block, size_t n) {
     const uint32_t* dtok = reinterpret_cast<const uint32_t*>(stage_.as<int>() + 1);
     forward_chunk(block, dtok, n, n, false, dtok);
     if (!direct) HIPC(hipMemcpyAsync(h_ctl_.p, ctl_.p, CTL_BACK * 4, hipMemcpyDeviceToHost, stream_));
+}
+
+size_t Model::debug_timeline(uint64_t* out, size_t cap) {
+    if (!pass_tl_.p) return 0;
+    HIPC(hipStreamSynchronize(stream_));
+    const size_t words = pass_tl_.n / 8;
+    if (out && cap) HIPC(hipMemcpy(out, pass_tl_.p, std::min(cap, words) * 8, hipMemcpyDeviceToHost));
+    return words;
+}
+
+size_t Model::debug_read(const char* name, void* out, size_t cap) {
+    const std::string n(name ? name : "");
+    const DevBuf* b = n == "x" ? &x_ : n == "xf" ? &xf_ : n == "ss" ? &ss_ : n == "q" ? &q_ : n == "af" ? &af_ : n == "actf" ? &actf_
+                    : n == "kcache" ? &kcache_ : n == "vcache" ? &vcache_ : n == "pass_area" ? &pass_area_ : nullptr;
+    if (!b) fail("no device buffer named '" + n + "'");
+    HIPC(hipStreamSynchronize(stream_));
+    if (out && cap && b->p) HIPC(hipMemcpy(out, b->p, std::min(cap, b->n), hipMemcpyDeviceToHost));
+    return b->n;
 }
 
 void Model::arm_failure() {

@@ -10,6 +10,7 @@
 #include "common.hpp"
 #include "fused.hpp"
 #include "kernels.hpp"
+#include "pass.hpp"
 #include "source.hpp"
 
 namespace ls {
@@ -142,6 +143,11 @@ public:
     ls_kernel_stat read_profile();
     // Test hook: the next device pass starts with the control block's error word set.
     void debug_fail_next() { fail_next_ = true; }
+    // Per-unit stamps of the last persistent pass (LS_PASS_TIMELINE=1), copied to out (cap
+    // words); returns the words available (0 without a timeline).
+    size_t debug_timeline(uint64_t* out, size_t cap);
+    // A copy of an internal device buffer (debugging): returns its size in bytes, copies up to cap.
+    size_t debug_read(const char* name, void* out, size_t cap);
 
 private:
     void check_request(const uint32_t* tok, size_t n) const;
@@ -182,6 +188,12 @@ private:
     DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, ctl_, bacc_;
     // Resident models: every layer's pointers for the layer-stack launch (LayerPtrs per layer).
     DevBuf layer_ptrs_;
+    // The persistent pass (one-tile passes over resident layers; LS_PASS=0: the layer stack): its
+    // exchange area, flag lines and epoch word (bumped by the embedding kernel before each pass),
+    // and per-unit timeline stamps when LS_PASS_TIMELINE=1.
+    bool pass_on_ = false;
+    DevBuf pass_area_, pass_flags_, epoch_, pass_tl_;
+    PassArea pass_shape_;
     PinnedBuf h_stage_, h_out_, h_ctl_, h_bacc_;
     // Control block: FLOW_WORDS words of fused-launch counters, then the acceptance (m, next).
     static constexpr int CTL_BACK = FLOW_ACC + 2;  // control words copied back after a pass: error, acceptance

@@ -457,11 +457,13 @@ def env(name, value):
 
 def test_layer_stack_and_per_layer_launches_give_identical_bits():
     """One-tile passes run every layer in one launch (k_layers) by default; LS_STACK=0 runs the
-    per-layer launches. Same plans, so the same logits bit for bit, and the same acceptance."""
+    per-layer launches. Same plans, so the same logits bit for bit, and the same acceptance. The
+    0.5B shape in every weight format (the tiny model is too narrow for the stack and runs the
+    per-layer launches either way)."""
     block = [8, 9, 400, 33, 120, 5, 77, 301, 2]
-    cases = [(name, tiny(name), PROMPT, 128) for name in ("bf16", "int8", "int4")]
     rng = np.random.default_rng(3)
-    cases.append(("0.5B int8", qwen05b((8, 64)), rng.integers(0, 151936, 40).tolist(), 256))
+    cases = [("0.5B " + name, qwen05b(fmt), rng.integers(0, 151936, 40).tolist(), 256)
+             for name, fmt in (("bf16", None), ("int8", (8, 64)), ("int4", (4, 32)))]
     for name, m, prompt, max_ctx in cases:
         say("stack vs per-layer", name)
         with env("LS_STACK", "0"):
