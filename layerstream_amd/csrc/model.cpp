@@ -17,6 +17,10 @@
 
 #include <chrono>
 #include <cmath>
+#include <condition_variable>
+#include <deque>
+#include <mutex>
+#include <thread>
 #include <cstdio>
 #include <cstdlib>
 
@@ -237,6 +241,13 @@ class StreamProvider : public DeviceProvider {
         PinnedBuf stage;
         hipEvent_t copied = nullptr, consumed = nullptr;
         bool used = false;
+        uint64_t read_seq = 0;  // the read-ahead request that fills stage with the next item
+    };
+    // A read of one item's bytes into a landing buffer's pinned stage, by the I/O thread.
+    struct Read {
+        Item it;
+        size_t landing;
+        uint64_t seq;
     };
 
 public:
@@ -270,8 +281,22 @@ public:
         embed_stage_ = PinnedBuf(max_rows_ * rb);
         embed_raw_ = DevBuf(max_rows_ * rb);
         HIPC(hipEventCreateWithFlags(&embed_copied_, hipEventDisableTiming));
+        // Bytes that are not already in pinned memory are read by an I/O thread, ahead of the
+        // copies in schedule order (src/provider.rs:187-206, 288-305).
+        if (!src_.pinned()) {
+            HIPC(hipGetDevice(&device_));
+            reader_ = std::thread([this] { read_loop(); });
+        }
     }
     ~StreamProvider() override {
+        if (reader_.joinable()) {
+            {
+                std::lock_guard<std::mutex> g(mu_);
+                stop_ = true;
+            }
+            cv_.notify_all();
+            reader_.join();
+        }
         (void)hipStreamSynchronize(copy_);
         (void)hipStreamSynchronize(build_);
         (void)hipStreamSynchronize(compute_);
@@ -304,6 +329,16 @@ public:
         next_take_ = 0;
         ahead_ = 0;
         holding_ = false;
+        if (reader_.joinable()) {
+            // Each pass reads its own items (as the reference counts them); reads a pass that did
+            // not end normally requested finish first and are forgotten.
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return (reads_.empty() && done_seq_ == read_seq_) || !read_error_.empty(); });
+            }
+            next_read_ = 0;
+            read_ahead();
+        }
         while (next_issue_ < schedule_.size() && next_issue_ < slots_.size()) issue();
     }
 
@@ -382,11 +417,15 @@ private:
         if (src_.pinned()) {
             from = it.kind == LAYER ? src_.layer_view(it.idx) : src_.embed_view() + first * rb;
         } else {
+            // The I/O thread has this item's read (requested read-ahead items back); wait for it.
+            read_ahead();
             auto t0 = std::chrono::steady_clock::now();
-            HIPC(hipEventSynchronize(d.copied));  // the staging buffer's previous copy has landed
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return done_seq_ >= d.read_seq || !read_error_.empty(); });
+                if (!read_error_.empty()) fail("streamed read failed: " + read_error_, LS_E_IO);
+            }
             wait_ns_ += uint64_t(std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0).count());
-            if (it.kind == LAYER) src_.read_layer(it.idx, d.stage.as<uint8_t>());
-            else src_.read_embed_rows(first, rows, d.stage.as<uint8_t>());
             from = d.stage.as<uint8_t>();
         }
         // The landing buffer is free once the rearrangement of its previous item has read it
@@ -411,6 +450,57 @@ private:
         s.used = true;
         d.used = true;
         next_issue_++;
+    }
+
+    // Requests reads for the schedule's items up to one landing buffer per item ahead of the next
+    // copy (a landing's stage is refilled once its previous copy has landed).
+    void read_ahead() {
+        bool any = false;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            while (next_read_ < schedule_.size() && next_read_ < next_issue_ + landing_.size()) {
+                Landing& d = landing_[next_read_ % landing_.size()];
+                d.read_seq = ++read_seq_;
+                reads_.push_back({schedule_[next_read_], next_read_ % landing_.size(), d.read_seq});
+                next_read_++;
+                any = true;
+            }
+        }
+        if (any) cv_.notify_all();
+    }
+
+    void read_loop() {
+        (void)hipSetDevice(device_);
+        for (;;) {
+            Read r;
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return stop_ || !reads_.empty(); });
+                if (stop_) return;
+                r = reads_.front();
+                reads_.pop_front();
+            }
+            Landing& d = landing_[r.landing];
+            std::string err;
+            try {
+                // the stage's previous copy has landed before it is overwritten
+                if (hipEventSynchronize(d.copied) != hipSuccess) throw std::runtime_error("waiting for a staging copy failed");
+                if (r.it.kind == LAYER) {
+                    src_.read_layer(r.it.idx, d.stage.as<uint8_t>());
+                } else {
+                    const size_t first = r.it.idx * STREAM_HEAD_ROWS;
+                    src_.read_embed_rows(first, std::min(STREAM_HEAD_ROWS, c_.vocab - first), d.stage.as<uint8_t>());
+                }
+            } catch (const std::exception& e) {
+                err = e.what();
+            }
+            {
+                std::lock_guard<std::mutex> g(mu_);
+                if (!err.empty() && read_error_.empty()) read_error_ = err;
+                done_seq_ = r.seq;
+            }
+            cv_.notify_all();
+        }
     }
 
     Slot& take(const Item& want) {
@@ -454,6 +544,16 @@ private:
     DevBuf embed_raw_;
     hipEvent_t embed_copied_ = nullptr;
     uint64_t wait_ns_ = 0, h2d_bytes_ = 0;
+    // the I/O thread (sources not in pinned memory)
+    std::thread reader_;
+    int device_ = 0;
+    std::mutex mu_;
+    std::condition_variable cv_;
+    std::deque<Read> reads_;
+    size_t next_read_ = 0;  // the next schedule item whose read is requested
+    uint64_t read_seq_ = 0, done_seq_ = 0;
+    bool stop_ = false;
+    std::string read_error_;
 };
 
 std::unique_ptr<DeviceProvider> make_resident(const Source& src, hipStream_t s) {
