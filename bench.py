@@ -74,6 +74,31 @@ def calibrate_copy(mib, reps=8):
     print(json.dumps({"calibration": "device-to-device copy", "bytes_read": n, "bytes_written": n, "reps": reps}), flush=True)
 
 
+PCIE_PEAK_GBS = 64.0  # the host link of one MI355X: PCIe 5.0 x16, one direction
+
+
+def measure_h2d(mib=256, reps=6):
+    """Best rate of one large copy from pinned host memory to the device (GB/s): what the link
+    gives a single copy, against which the streamed passes' rate is read."""
+    h = C.CDLL("libamdhip64.so")
+    n = mib << 20
+    host, dev = C.c_void_p(), C.c_void_p()
+    if h.hipHostMalloc(C.byref(host), C.c_size_t(n), 0) or h.hipMalloc(C.byref(dev), C.c_size_t(n)):
+        raise RuntimeError("allocation for the link measurement failed")
+    C.memset(host, 1, n)
+    best = 0.0
+    for i in range(reps + 1):
+        t0 = time.perf_counter()
+        if h.hipMemcpy(dev, host, C.c_size_t(n), 1):  # hipMemcpyHostToDevice
+            raise RuntimeError("hipMemcpy failed")
+        dt = time.perf_counter() - t0
+        if i:
+            best = max(best, n / dt / 1e9)
+    h.hipFree(dev)
+    h.hipHostFree(host)
+    return best
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -294,6 +319,9 @@ def main():
     ap.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel-trace CSV of a bench run and exit")
     ap.add_argument("--pmc-summary", metavar="CSV", help="summarise a rocprofv3 counter-collection CSV of a bench run and exit")
     ap.add_argument("--last", type=int, default=ROOF_STEPS, help="verify steps the summaries cover (the last ones of the run)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time the prefill of the config's prompt (C2: 512 tokens, C3: 2048) instead of verify steps; "
+                    "prints a prefill throughput line with an MFMA roofline")
     ap.add_argument("--stage-timeline", action="store_true",
                     help="run the workload through the persistent layer pass (LS_PASS=1) with its per-unit timeline and print a "
                     "per-stage summary of the last verify step instead of the JSON line")
@@ -323,7 +351,11 @@ def main():
             sys.exit("--stage-timeline takes a single-sequence workload")
         os.environ["LS_PASS"] = "1"
         os.environ["LS_PASS_TIMELINE"] = "1"
-    if conf["batch"] > 1:
+    if args.prefill:
+        if conf["batch"] > 1 or conf["prompt"] < 1:
+            sys.exit("--prefill takes a single-sequence workload with a prompt")
+        run_prefill(args, conf)
+    elif conf["batch"] > 1:
         run_batch(args, conf)
     else:
         run_single(args, conf)
@@ -456,11 +488,17 @@ def run_single(args, conf):
     }
     if args.mode == "stream":
         h2d = rep1["h2d_bytes"] - rep0["h2d_bytes"]
+        link = measure_h2d()
         res["stream"] = {
             "h2d_bytes_per_step": int(h2d / K),
             "h2d_GBps": round(h2d / wall / 1e9, 2),
+            "link_one_copy_GBps": round(link, 2),
+            "link_peak_GBps": PCIE_PEAK_GBS,
+            "h2d_frac_of_one_copy": round(h2d / wall / 1e9 / link, 4),
+            "h2d_frac_of_peak": round(h2d / wall / 1e9 / PCIE_PEAK_GBS, 4),
             "host_wait_ms_per_step": round((rep1["wait_ns"] - rep0["wait_ns"]) / K / 1e6, 4),
-            "note": "weights cross PCIe from pinned host memory every pass (2 device slots)",
+            "note": "weights cross PCIe every pass (2 device slots) from a pinned copy kept in the tile layout; "
+            "link_one_copy_GBps: the best single 256 MiB pinned-to-device copy in this process",
         }
     if not args.no_cpu:
         t0 = time.time()
@@ -469,6 +507,100 @@ def run_single(args, conf):
         log(f"cpu baseline {time.time() - t0:.1f}s")
     run.close()
     drafter.close()
+    print(json.dumps(res), flush=True)
+
+
+MFMA_BF16_PEAK_TFS = 2500.0  # dense bf16 MFMA, MI355X
+PREFILL_CHUNK = 128  # tokens per prefill pass (src/model.rs:14)
+
+
+def prefill_flops(cfg, t):
+    """Algorithmic flops of prefilling t tokens: the layer matrices for every token, causal
+    attention (q.k and p.v), and the head for the last token (forward returns its logits)."""
+    h, inter, hd = cfg["hidden"], cfg["inter"], cfg["head_dim"]
+    qd, kvd = cfg["heads"] * hd, cfg["kv_heads"] * hd
+    per_layer = h * (qd + 2 * kvd) + qd * h + 3 * inter * h
+    attn = 4 * hd * cfg["heads"] * t * (t + 1) / 2
+    return cfg["layers"] * (2 * t * per_layer + attn) + 2 * cfg["vocab"] * h
+
+
+def run_prefill(args, conf):
+    """Prefill throughput: the config's prompt through 128-token passes (each a chain of matrix
+    launches over eight 16-token tiles, bf16 MFMA on three-term splits), timed from the call to
+    the last position's logits on the host; the model is reset between repetitions."""
+    import layerstream_amd as LS
+
+    text, parts, img, src = workload_source(conf, "resident")
+    cfg = src.config()
+    _, layer_bytes = LS.layer_layout(text)
+    row_bytes = LS.row_bytes(cfg["embed_format"], cfg["hidden"])
+    T = conf["prompt"]
+    rng = np.random.default_rng(512)
+    prompt = rng.integers(0, cfg["vocab"], T).tolist()
+    model = LS.Model(src, LS.MODE_RESIDENT, 2, T + 8)
+    W, K = max(1, min(args.warmup, 3)), max(2, min(args.steps, 10))
+    for _ in range(W):
+        model.forward(prompt)
+        model.reset()
+    hip_sync()
+    times = []
+    for _ in range(K):
+        t0 = time.perf_counter()
+        model.forward(prompt)
+        times.append(time.perf_counter() - t0)
+        model.reset()
+    sec = float(np.median(times))
+    flops = prefill_flops(cfg, T)
+    chunks = -(-T // PREFILL_CHUNK)
+    # each 128-token pass reads every layer's weights once; the head reads the table once
+    hbm = chunks * cfg["layers"] * layer_bytes + cfg["vocab"] * row_bytes
+    res = {
+        "metric": "prefill tok/s at 1 GPU; % MFMA roofline",
+        "value": round(T / sec, 1),
+        "unit": "prompt tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"prefill of {T} random ids, {args.config}'s model: {describe(conf)}; 128-token passes",
+                   "prompt": T},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(flops / sec / 1e12, 2),
+            "peak": MFMA_BF16_PEAK_TFS,
+            "unit": "TFLOP/s",
+            "frac": round(flops / sec / 1e12 / MFMA_BF16_PEAK_TFS, 4),
+            "traffic": None,
+            "flops_per_prefill": int(flops),
+            "note": "algorithmic flops (matrices, causal attention, the head for the last token) over the whole prefill; the "
+            "MFMAs run three bf16 terms per f32 activation, so the instruction count is about 3x these flops",
+        },
+        "hbm": {"algorithmic_bytes": int(hbm), "GBps": round(hbm / sec / 1e9, 1), "frac": round(hbm / sec / 1e9 / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        # The oracle's prefill of a bounded sample (the first 128 tokens: one pass) on the host.
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle_py as O
+
+        cparts = parts if img is None else split_parts(img, cfg)
+        ocfg = {kk: cfg[kk] for kk in ("format", "embed_format", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "vocab", "eps",
+                                       "rope_theta")}
+        cores = len(os.sched_getaffinity(0))
+        n = min(T, PREFILL_CHUNK)
+        om = O.OracleModel(ocfg, cparts["layers"], cparts["embed"], cparts["norm"], threads=cores, max_ctx=n + 8)
+        t0 = time.perf_counter()
+        om.forward(prompt[:n])
+        cs = time.perf_counter() - t0
+        om.close()
+        res["cpu_baseline"] = {"value": round(n / cs, 2), "unit": "prompt tok/s", "cores": cores, "kind": "port",
+                               "sample": f"prefill of the first {n} of the {T} prompt tokens (one 128-token pass), {cs:.1f}s; C "
+                               f"restatement of the reference CPU path, {cores} threads"}
     print(json.dumps(res), flush=True)
 
 

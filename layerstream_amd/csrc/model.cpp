@@ -281,6 +281,14 @@ public:
         embed_stage_ = PinnedBuf(max_rows_ * rb);
         embed_raw_ = DevBuf(max_rows_ * rb);
         HIPC(hipEventCreateWithFlags(&embed_copied_, hipEventDisableTiming));
+        // Bytes already in pinned memory: a pinned mirror of every item in the tile layout,
+        // built once here, so that each pass copies straight into the slots (LS_STREAM_TILED=0:
+        // copy the source's bytes and rearrange them on the device every pass).
+        if (src_.pinned()) {
+            tiled_on_ = true;
+            if (const char* e = std::getenv("LS_STREAM_TILED")) tiled_on_ = std::atoi(e) != 0;
+            if (tiled_on_) build_tiled();
+        }
         // Bytes that are not already in pinned memory are read by an I/O thread, ahead of the
         // copies in schedule order (src/provider.rs:187-206, 288-305).
         if (!src_.pinned()) {
@@ -400,9 +408,57 @@ public:
     }
 
 private:
+    size_t head_data_bytes() const { return tile_data_bytes(hshape_); }
+    size_t head_scale_bytes() const { return std::max<size_t>(16, tile_scale_bytes(hshape_)); }
+    size_t tiled_head_off() const { return c_.layers * a_.total; }
+
+    // The pinned mirror: each layer's arena, then each head chunk's tile data and scales, made by
+    // the same device rearrangement a pass would run (so the slots get the same bytes).
+    void build_tiled() {
+        const size_t hd = head_data_bytes(), hs = head_scale_bytes(), rb = c_.row_bytes();
+        tiled_ = PinnedBuf(tiled_head_off() + n_head_chunks() * (hd + hs));
+        Slot& s = slots_[0];
+        Landing& d = landing_[0];
+        uint8_t* dst = tiled_.as<uint8_t>();
+        for (size_t l = 0; l < c_.layers; l++) {
+            HIPC(hipMemcpyAsync(d.raw.p, src_.layer_view(l), L_.total, hipMemcpyHostToDevice, copy_));
+            build_layer_device(c_, L_, d.raw.as<uint8_t>(), a_, s.arena.as<uint8_t>(), copy_);
+            HIPC(hipMemcpyAsync(dst + l * a_.total, s.arena.p, a_.total, hipMemcpyDeviceToHost, copy_));
+        }
+        for (size_t c = 0; c < n_head_chunks(); c++) {
+            const size_t first = c * STREAM_HEAD_ROWS, rows = head_rows(c);
+            HIPC(hipMemcpyAsync(d.raw.p, src_.embed_view() + first * rb, rows * rb, hipMemcpyHostToDevice, copy_));
+            TMat m = tile_bind(hshape_, s.hdata.as<uint8_t>(), s.hscales.as<uint16_t>());
+            tile_repack(d.raw.as<uint8_t>(), int(rows), m, 0, int(rows), int(rows), copy_);
+            uint8_t* at = dst + tiled_head_off() + c * (hd + hs);
+            HIPC(hipMemcpyAsync(at, s.hdata.p, hd, hipMemcpyDeviceToHost, copy_));
+            HIPC(hipMemcpyAsync(at + hd, s.hscales.p, hs, hipMemcpyDeviceToHost, copy_));
+        }
+        HIPC(hipStreamSynchronize(copy_));
+    }
+
     void issue() {
         const Item it = schedule_[next_issue_];
         Slot& s = slots_[next_issue_ % slots_.size()];
+        if (tiled_on_) {
+            // Straight from the pinned mirror into the slot, once compute is done with it.
+            if (s.used) HIPC(hipStreamWaitEvent(copy_, s.freed, 0));
+            const uint8_t* mirror = tiled_.as<uint8_t>();
+            if (it.kind == LAYER) {
+                HIPC(hipMemcpyAsync(s.arena.p, mirror + it.idx * a_.total, a_.total, hipMemcpyHostToDevice, copy_));
+                h2d_bytes_ += a_.total;
+            } else {
+                const size_t hd = head_data_bytes(), hs = head_scale_bytes();
+                const uint8_t* at = mirror + tiled_head_off() + it.idx * (hd + hs);
+                HIPC(hipMemcpyAsync(s.hdata.p, at, hd, hipMemcpyHostToDevice, copy_));
+                HIPC(hipMemcpyAsync(s.hscales.p, at + hd, hs, hipMemcpyHostToDevice, copy_));
+                h2d_bytes_ += hd + hs;
+            }
+            HIPC(hipEventRecord(s.ready, copy_));
+            s.used = true;
+            next_issue_++;
+            return;
+        }
         Landing& d = landing_[next_issue_ % landing_.size()];
         const size_t rb = c_.row_bytes();
         size_t bytes, first = 0, rows = 0;
@@ -544,6 +600,8 @@ private:
     DevBuf embed_raw_;
     hipEvent_t embed_copied_ = nullptr;
     uint64_t wait_ns_ = 0, h2d_bytes_ = 0;
+    bool tiled_on_ = false;  // copies from the pinned tile-layout mirror
+    PinnedBuf tiled_;
     // the I/O thread (sources not in pinned memory)
     std::thread reader_;
     int device_ = 0;

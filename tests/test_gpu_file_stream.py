@@ -82,3 +82,29 @@ def test_a_file_that_shrinks_under_the_model_is_an_error(tmp_path):
     with pytest.raises(LS.LayerstreamError) as e:
         g.forward([1])
     assert e.value.code == -3
+
+
+@pytest.mark.parametrize("name", ["int4", "mixed"])
+def test_pinned_streaming_from_the_tiled_mirror_gives_the_resident_bits(name):
+    """A pinned source is streamed from a pinned copy already in the tile layout (built once by the
+    provider, no rearrangement per pass); LS_STREAM_TILED=0 copies the source's own bytes and
+    rearranges them on the device every pass. Both give the resident logits bit for bit, for 1, 2
+    and 3 slots, and the reads are counted the same way."""
+    from test_gpu import env
+
+    m = tiny(name)
+    ref = run_fixed(gpu_model(m))
+    img = np.frombuffer(bytes(m["lsq"]), np.uint8).copy()
+    for tiled in ("1", "0"):
+        for slots in (1, 2, 3):
+            say("pinned stream", name, "tiled", tiled, "slots", slots)
+            src = LS.Source.from_lsq_image(img).pinned_copy()
+            with env("LS_STREAM_TILED", tiled):
+                g = LS.Model(src, LS.MODE_STREAM, slots, 128)
+            got = run_fixed(g)
+            assert np.array_equal(bits(ref), bits(got)), (name, tiled, slots)
+            c = src.config()
+            _, total = LS.layer_layout(m["config_text"])
+            rb = LS.row_bytes(c["embed_format"], c["hidden"])
+            passes = 1 + len(FOLLOW)
+            assert src.bytes_read() == passes * (c["layers"] * total + c["vocab"] * rb) + (len(PROMPT) + len(FOLLOW)) * rb
