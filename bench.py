@@ -118,6 +118,9 @@ CONFIGS = {
     "C3": dict(model="0.5b", fmt=(4, 32), prompt=2048, k=8, batch=1),
     "C4": dict(model="0.5b", fmt=(8, 64), prompt=0, k=8, batch=16),  # prompts of U[128, 1024] ids
     "C5": dict(model="3b", fmt=(8, 64), prompt=1024, k=8, batch=1),
+    # C2 with a real draft model: the same seeded weights quantized to int4-g32, resident on the
+    # same GPU; its kk proposals per step run as one chain of device passes.
+    "C2D": dict(model="0.5b", fmt=(8, 64), prompt=512, k=8, batch=1, draft_fmt=(4, 32)),
 }
 FMT_NAME = {16: "bf16", 8: "int8", 4: "int4"}
 
@@ -205,6 +208,35 @@ def cpu_baseline(parts, cfg, prompt, drafter_g, p_accept, seed, k, n_steps, gpu_
         "accepted_match_gpu": ms_acc == list(gpu_m[: len(ms_acc)]),
         "tokens_match_gpu": emitted == list(gpu_tokens[: len(emitted)]),
         "tokens_compared": len(emitted),
+    }
+
+
+def cpu_baseline_draft(parts, dparts, cfg, dcfg, prompt, k, gpu_tokens, max_new=25):
+    """The oracle's speculative_greedy with the oracle draft model on the host cores: both models
+    prefill the prompt (untimed), then max_new tokens; verified tok/s over the decode time, and the
+    tokens compared with the GPU run's."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_py as O
+
+    keys = ("format", "embed_format", "hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "vocab", "eps", "rope_theta")
+    cores = len(os.sched_getaffinity(0))
+    ctx = len(prompt) + max_new + k + 8
+    tm = O.OracleModel({kk: cfg[kk] for kk in keys}, parts["layers"], parts["embed"], parts["norm"], threads=cores, max_ctx=ctx)
+    dm = O.OracleModel({kk: dcfg[kk] for kk in keys}, dparts["layers"], dparts["embed"], dparts["norm"], threads=cores, max_ctx=ctx)
+    toks, st = O.speculative_greedy(tm, O.model_drafter(dm), prompt, max_new, k)
+    tm.close()
+    dm.close()
+    return {
+        "value": round((len(toks) - 1) / st["decode_secs"], 3),
+        "unit": "verified tok/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"both models prefill {len(prompt)} tokens (untimed, {st['first_secs']:.1f}s), then {max_new} tokens of "
+        f"speculative_greedy with k={k} (decode {st['decode_secs']:.1f}s, {st['target_passes']} target passes); C restatement "
+        f"of the reference CPU path, {cores} threads",
+        "acceptance": round(st["accepted"] / max(st["drafted"], 1), 4),
+        "tokens_match_gpu": toks == list(gpu_tokens[: len(toks)]),
+        "tokens_compared": len(toks),
     }
 
 
@@ -407,8 +439,15 @@ def run_single(args, conf):
     model.reset()
     log(f"greedy reference {len(g)} tokens in {time.time() - t0:.1f}s")
     seed = 2024
-    drafter = LS.ScriptedDrafter(g, args.p_accept, seed, cfg["vocab"])
+    draft_model = None
+    if conf.get("draft_fmt"):
+        _, dparts, dimg, dsrc = workload_source(dict(conf, fmt=conf["draft_fmt"]), "resident")
+        draft_model = LS.Model(dsrc, LS.MODE_RESIDENT, 2, max_ctx)
+        drafter = LS.ModelDrafter(draft_model)
+    else:
+        drafter = LS.ScriptedDrafter(g, args.p_accept, seed, cfg["vocab"])
     run = LS.SpecRun(model, drafter, prompt, max_new, k)
+    st0 = run.stats()
     run.step(W)
     hip_sync()
     rep0 = model.report()
@@ -417,6 +456,7 @@ def run_single(args, conf):
     hip_sync()
     wall = time.perf_counter() - t0
     rep1 = model.report()
+    st1 = run.stats()
     if args.stage_timeline:
         tl = model.debug_timeline()
         if tl is None:
@@ -468,8 +508,10 @@ def run_single(args, conf):
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: {describe(conf)}; prompt {conf['prompt']} random ids; k={k} chain drafts, scripted "
-            f"{round(100 * args.p_accept)}% per-token acceptance; greedy verify",
+            "workload": f"{args.config}: {describe(conf)}; prompt {conf['prompt']} random ids; k={k} chain drafts, "
+            + (f"from a {fmt_tag(conf['draft_fmt'])} draft of the same weights (resident, proposals chained on the device)"
+               if conf.get("draft_fmt") else f"scripted {round(100 * args.p_accept)}% per-token acceptance")
+            + "; greedy verify",
             "mode": args.mode,
             "k": k,
             "ctx_start": ctx0,
@@ -486,6 +528,16 @@ def run_single(args, conf):
         "roofline": roofline,
         "cpu_baseline": None,
     }
+    if draft_model is not None:
+        dd = {f: st1[f] - st0[f] for f in ("drafted", "accepted", "draft_forwards", "target_passes", "draft_secs", "target_secs")}
+        res["draft"] = {
+            "format": fmt_tag(conf["draft_fmt"]),
+            "acceptance": round(dd["accepted"] / max(dd["drafted"], 1), 4),
+            "draft_ms_per_step": round(dd["draft_secs"] / max(dd["target_passes"], 1) * 1e3, 4),
+            "target_ms_per_step": round(dd["target_secs"] / max(dd["target_passes"], 1) * 1e3, 4),
+            "draft_forwards_per_step": round(dd["draft_forwards"] / max(dd["target_passes"], 1), 3),
+            "note": "a step's kk proposals are one graph of kk one-token passes of the draft, one host wait",
+        }
     if args.mode == "stream":
         h2d = rep1["h2d_bytes"] - rep0["h2d_bytes"]
         link = measure_h2d()
@@ -503,7 +555,11 @@ def run_single(args, conf):
     if not args.no_cpu:
         t0 = time.time()
         cparts = parts if img is None else split_parts(img, cfg)
-        res["cpu_baseline"] = cpu_baseline(cparts, cfg, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m), out_tokens)
+        if draft_model is not None:
+            dcparts = dparts if dimg is None else split_parts(dimg, cfg)
+            res["cpu_baseline"] = cpu_baseline_draft(cparts, dcparts, cfg, dsrc.config(), prompt, k, out_tokens)
+        else:
+            res["cpu_baseline"] = cpu_baseline(cparts, cfg, prompt, g, args.p_accept, seed, k, args.cpu_steps, list(m), out_tokens)
         log(f"cpu baseline {time.time() - t0:.1f}s")
     run.close()
     drafter.close()

@@ -147,6 +147,13 @@ int ls_model_forward_multi(ls_model* m, const uint32_t* tokens, size_t n, size_t
  * src/spec.rs:137-139. Only *accepted (m) and *next (the correction or bonus token) return
  * to the host. */
 int ls_model_verify_greedy(ls_model* m, const uint32_t* block, size_t n, uint32_t* accepted, uint32_t* next);
+/* A draft model's proposals (src/spec.rs:100-107: kk single-token forwards, each fed the argmax
+ * of the one before): out[i] is the argmax after consuming first, out[0] .. out[i - 1], and the
+ * model advances by k positions, exactly as k calls of ls_model_forward with argmax. Over resident
+ * weights the k passes run chained on the device with one host wait (LS_E_STATE otherwise);
+ * 1 <= k <= 32. The reference has no such call: its draft loop sits inside speculative_greedy;
+ * here the model drafter (ls_drafter_from_model) runs that loop through this call. */
+int ls_model_draft_chain(ls_model* m, uint32_t first, size_t k, uint32_t* out);
 
 /* Several independent sequences over one copy of the weights. The reference has one KV cache
  * per Model (src/model.rs:16-26, 67-68); this model holds n_seq of them (each max_ctx tokens)

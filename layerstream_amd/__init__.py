@@ -134,6 +134,7 @@ SIGNATURES = {
     "ls_model_verify_greedy": (C.c_int, [P, U32, SZ, U32, U32]),
     "ls_model_report": (C.c_int, [P, C.POINTER(Report)]),
     "ls_model_last_step_ms": (C.c_double, [P]),
+    "ls_model_draft_chain": (C.c_int, [P, C.c_uint32, SZ, U32]),
     "ls_drafter_from_model": (C.c_int, [P, C.POINTER(Drafter)]),
     "ls_drafter_scripted": (C.c_int, [U32, SZ, C.c_double, C.c_uint64, C.c_uint64, C.POINTER(Drafter)]),
     "ls_drafter_scripted_token": (C.c_uint32, [C.POINTER(Drafter), SZ]),
@@ -454,6 +455,13 @@ class Model:
         out = np.zeros(n, np.uint8)
         lib().ls_model_debug_read(self.h, name.encode(), out.ctypes.data, n)
         return out
+
+    def draft_chain(self, first: int, k: int) -> list:
+        """k greedy single-token passes chained on the device: the draft model's proposals after
+        `first` (the same tokens as k forward + argmax calls); the model advances by k."""
+        out = np.zeros(k, np.uint32)
+        _check(lib().ls_model_draft_chain(self.h, first, k, _u32(out)))
+        return out.tolist()
 
     def debug_fail_next(self):
         """Test hook: the next device pass starts with its error word set and fails with

@@ -281,6 +281,15 @@ int ls_model_verify_greedy(ls_model* m, const uint32_t* block, size_t n, uint32_
     });
 }
 
+int ls_model_draft_chain(ls_model* m, uint32_t first, size_t k, uint32_t* out) {
+    return guard([&] {
+        need(m, "model");
+        need(out, "output");
+        if (k < 1 || k > 32) ls::fail("a draft chain takes 1 to 32 passes, not " + std::to_string(k));
+        m->m->draft_chain(first, k, out);
+    });
+}
+
 int ls_model_report(const ls_model* m, ls_report* out) {
     return guard([&] {
         need(m, "model");

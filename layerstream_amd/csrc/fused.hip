@@ -1575,6 +1575,21 @@ __global__ void k_accept_batch(const uint32_t* __restrict__ amax, const uint32_t
     if (blockIdx.x == 0 && threadIdx.x == 0) out[0] = uint32_t(ctl[FLOW_ERR]);
 }
 
+__global__ void k_chain_step(const int* __restrict__ ctl, int* __restrict__ stage, uint32_t* __restrict__ out, int i, int n) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const int next = ctl[FLOW_ACC + 1];
+        out[i] = uint32_t(next);
+        out[n] = uint32_t(ctl[FLOW_ERR]);
+        stage[0] += 1;
+        stage[1] = next;
+    }
+}
+
+void chain_step(const int* ctl, int* stage, uint32_t* out, int i, int n, hipStream_t s) {
+    hipLaunchKernelGGL(k_chain_step, dim3(1), dim3(64), 0, s, ctl, stage, out, i, n);
+    FCHECK(hipGetLastError());
+}
+
 void accept_greedy_batch(const uint32_t* amax, const uint32_t* tok, const int* first, const int* len, int n_seq, const int* ctl,
                          uint32_t* out, hipStream_t s) {
     hipLaunchKernelGGL(k_accept_batch, dim3(1), dim3(256), 0, s, amax, tok, first, len, n_seq, ctl, out);

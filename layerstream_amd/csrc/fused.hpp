@@ -289,5 +289,9 @@ void head_argmax_final(const float* pv, const int* pi, int arg_stride, int nbloc
 // out = [ctl[FLOW_ERR], m_0, next_0, m_1, next_1, ...].
 void accept_greedy_batch(const uint32_t* amax, const uint32_t* tok, const int* first, const int* len, int n_seq, const int* ctl,
                          uint32_t* out, hipStream_t s);
+// One link of a draft chain, after a one-token verify pass: the pass's greedy token
+// (ctl[FLOW_ACC + 1]) becomes out[i] and the next pass's input (stage[1]), whose position is one
+// more (stage[0] += 1); out[n] keeps the error word.
+void chain_step(const int* ctl, int* stage, uint32_t* out, int i, int n, hipStream_t s);
 
 }  // namespace ls

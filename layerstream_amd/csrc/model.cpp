@@ -626,6 +626,7 @@ std::unique_ptr<DeviceProvider> make_stream(const Source& src, int slots, size_t
 // ---------------------------------------------------------------------------------------
 constexpr size_t PREFILL_CHUNK = 128;  // src/model.rs:14
 constexpr size_t MAX_BLOCK = 33;       // a verify block: 1 + MAX_DRAFT (src/spec.rs:52) tokens
+constexpr size_t MAX_CHAIN = 32;       // a draft chain: at most MAX_DRAFT passes
 constexpr int MAX_SEQ = 1024;
 
 Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device, int n_seq)
@@ -742,6 +743,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     ctl_ = DevBuf(flow_words(int(c.layers)) * 4);
     HIPC(hipMemsetAsync(ctl_.p, 0, ctl_.n, stream_));
     bacc_ = DevBuf((1 + 2 * size_t(n_seq)) * 4);
+    chain_out_ = DevBuf((MAX_CHAIN + 1) * 4);
     h_stage_ = PinnedBuf(stage_words * 4);
     h_out_ = PinnedBuf(PREFILL_CHUNK * 4);
     h_ctl_ = PinnedBuf(CTL_BACK * 4);
@@ -796,6 +798,7 @@ Model::~Model() {
     if (stream_) (void)hipStreamSynchronize(stream_);
     for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
     for (auto& kv : batch_graphs_) (void)hipGraphExecDestroy(kv.second);
+    for (auto& kv : chain_graphs_) (void)hipGraphExecDestroy(kv.second);
     for (hipEvent_t e : prof_ev_) (void)hipEventDestroy(e);
     prov_.reset();
     if (ev0_) (void)hipEventDestroy(ev0_);
@@ -1366,6 +1369,71 @@ void Model::verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t
     *m = o[0];
     *next = o[1];
     pos_ = p + o[0] + 1;  // truncate(p + m + 1), src/spec.rs:137-139
+}
+
+// A draft chain: k one-token verify passes (a block of one token accepts nothing and gives the
+// argmax as `next`), each followed by chain_step, which makes that token the next pass's input
+// one position further on. The staged words start as (position, first) and live on the device.
+void Model::chain_body(size_t k) {
+    HIPC(hipMemcpyAsync(stage_.p, h_stage_.p, 2 * 4, hipMemcpyHostToDevice, stream_));
+    stage_pos_ = stage_.as<int>();
+    const uint32_t* dtok = reinterpret_cast<const uint32_t*>(stage_.as<int>() + 1);
+    for (size_t i = 0; i < k; i++) {
+        forward_chunk(nullptr, dtok, 1, 1, false, dtok);
+        chain_step(ctl_.as<int>(), stage_.as<int>(), chain_out_.as<uint32_t>(), int(i), int(k), stream_);
+    }
+    HIPC(hipMemcpyAsync(h_out_.p, chain_out_.p, (k + 1) * 4, hipMemcpyDeviceToHost, stream_));
+}
+
+void Model::draft_chain(uint32_t first, size_t k, uint32_t* out) {
+    HIPC(hipSetDevice(device_));
+    if (k == 0) return;
+    if (k > MAX_CHAIN) fail("a draft chain takes at most " + std::to_string(MAX_CHAIN) + " passes");
+    if (!prov_->resident()) fail("a draft chain runs over resident weights", LS_E_STATE);
+    check_request(&first, 1);
+    if (pos_ + k > max_ctx_) fail("the draft chain would pass the context limit");
+    const size_t p = pos_;
+    const std::pair<int, size_t> key(cur_, k);
+    chunk_index_ = 0;
+    h_stage_.as<int>()[0] = int(p);
+    h_stage_.as<uint32_t>()[1] = first;
+    arm_failure();
+    if (graphs_on_ && !prof_) {
+        auto it = chain_graphs_.find(key);
+        if (it == chain_graphs_.end()) {
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ge = nullptr;
+            HIPC(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            try {
+                chain_body(k);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream_, &g);
+                if (g) (void)hipGraphDestroy(g);
+                pos_ = p;
+                throw;
+            }
+            HIPC(hipStreamEndCapture(stream_, &g));
+            const hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            HIPC(e);
+            it = chain_graphs_.emplace(key, ge).first;
+        }
+        HIPC(hipGraphLaunch(it->second, stream_));
+    } else {
+        chain_body(k);
+    }
+    HIPC(hipStreamSynchronize(stream_));
+    harvest();
+    const uint32_t* o = h_out_.as<uint32_t>();
+    pos_ = p;
+    if (o[k]) {
+        // the same recovery as any pass whose in-launch wait gave up
+        int ctl[CTL_BACK] = {};
+        ctl[FLOW_ERR] = int(o[k]);
+        check_flow(ctl);
+    }
+    for (size_t i = 0; i < k; i++) out[i] = o[i];
+    pos_ = p + k;
 }
 
 // Batched verify: one pass over every sequence's block, rows in sequence order. Staging

@@ -133,6 +133,11 @@ public:
     void forward(const uint32_t* tok, size_t n, float* logits, uint32_t* argmax);
     void forward_multi(const uint32_t* tok, size_t n, size_t n_logits, float* logits, uint32_t* argmax);
     void verify_greedy(const uint32_t* block, size_t n, uint32_t* m, uint32_t* next);
+    // k greedy one-token passes chained on the device (a draft model's proposals, src/spec.rs:100-107):
+    // out[i] is the argmax after consuming first, out[0] .. out[i - 1]; the model advances by k.
+    // The same tokens as k calls of forward + argmax, with one host wait for all of them.
+    void draft_chain(uint32_t first, size_t k, uint32_t* out);
+    bool chains_on_device() const { return prov_->resident(); }
     ls_report report() const { return prov_->report(); }
     double last_step_ms() const { return last_step_ms_; }
     int device() const { return device_; }
@@ -163,6 +168,8 @@ private:
     // The device part of a verify step (token and position copies from the pinned staging
     // buffers, forward pass, acceptance, result copy): what a graph captures.
     void verify_body(const uint32_t* block, size_t n);
+    // The device part of a draft chain of k passes (what a graph captures).
+    void chain_body(size_t k);
     // The device part of a batched verify step; words: staged ints, n_segs: attention segments.
     void batch_body(const uint32_t* blocks, size_t rows, size_t words, int n_segs);
     void plan_kw_from_env();
@@ -223,6 +230,8 @@ private:
     bool fail_next_ = false;
     std::map<std::pair<int, size_t>, hipGraphExec_t> graphs_;  // verify step per (sequence, block length)
     std::map<std::vector<size_t>, hipGraphExec_t> batch_graphs_;  // batched verify step per block lengths
+    std::map<std::pair<int, size_t>, hipGraphExec_t> chain_graphs_;  // draft chain per (sequence, length)
+    DevBuf chain_out_;  // a draft chain's tokens, then its error word
     std::vector<hipEvent_t> prof_ev_;
     size_t prof_used_ = 0;
     ls_kernel_stat prof_acc_{};

@@ -25,8 +25,14 @@ static int md_prefill(void* ctx, const uint32_t* p, size_t n) {
     return 1;
 }
 
+// kk single-token passes, each fed the argmax of the one before (src/spec.rs:100-107). Over
+// resident weights they run as one chain on the device (one host wait for all kk tokens).
 static int md_propose(void* ctx, uint32_t last, size_t kk, uint32_t* out) {
     auto* m = static_cast<Model*>(ctx);
+    if (m->chains_on_device()) {
+        m->draft_chain(last, kk, out);
+        return int(kk);
+    }
     uint32_t cur = last;
     for (size_t i = 0; i < kk; i++) {
         m->forward(&cur, 1, nullptr, &out[i]);
