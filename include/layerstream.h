@@ -302,6 +302,51 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
 int ls_matmul_noalloc(ls_format f, const void* w_dev, size_t rows, size_t cols, const float* x_dev, size_t t,
                       float* y_dev, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Text and sampling around the engine, host side: the tokenizer (src/tokenizer.rs) and the
+ * sampler (src/model.rs:300-366).
+ * Variable-length outputs: *n (or *len) receives the full size; the data is copied only when
+ * out is not NULL and cap is at least that size (call again with a larger buffer otherwise).
+ * ------------------------------------------------------------------------------------- */
+typedef struct ls_tokenizer ls_tokenizer;
+/* Tokenizer::load (src/tokenizer.rs:67-180): vocab.json, merges.txt, tokenizer_config.json of
+ * dir. LS_E_IO when a file is missing, LS_E_FORMAT for bad content. */
+int ls_tokenizer_load(const char* dir, ls_tokenizer** out);
+void ls_tokenizer_free(ls_tokenizer* t);
+size_t ls_tokenizer_vocab_size(const ls_tokenizer* t);
+/* Tokenizer::encode (src/tokenizer.rs:208-232): text (UTF-8, len bytes; LS_E_INVALID if not
+ * valid UTF-8) to ids, added tokens such as <|im_start|> matched literally. */
+int ls_tokenizer_encode(const ls_tokenizer* t, const char* text, size_t len, uint32_t* out, size_t cap, size_t* n);
+/* Tokenizer::decode (src/tokenizer.rs:303-306): special tokens hidden, invalid UTF-8 replaced by
+ * U+FFFD. */
+int ls_tokenizer_decode(const ls_tokenizer* t, const uint32_t* ids, size_t n, char* out, size_t cap, size_t* len);
+/* Tokenizer::token_bytes (src/tokenizer.rs:289-301). */
+int ls_tokenizer_token_bytes(const ls_tokenizer* t, uint32_t id, int show_special, char* out, size_t cap, size_t* len);
+/* Tokenizer::token_id (src/tokenizer.rs:200-202): 1 and *id when the token exists, else 0. */
+int ls_tokenizer_token_id(const ls_tokenizer* t, const char* token, uint32_t* id);
+/* Tokenizer::is_special (src/tokenizer.rs:204-206). */
+int ls_tokenizer_is_special(const ls_tokenizer* t, uint32_t id);
+/* The pre-token split of text (src/tokenizer.rs:356-437; the Qwen2 pattern with the Unicode
+ * letter and number categories): ends[i] is the code point end of pre-token i. For tests. */
+int ls_tokenizer_pretokens(const char* text, size_t len, uint32_t* ends, size_t cap, size_t* n);
+
+/* StreamDecoder (src/tokenizer.rs:311-346): feed token bytes, get the text complete so far.
+ * out must hold 3 * (n + 4) bytes (no partial copies: the decoder's state moves on). */
+typedef struct ls_stream_decoder ls_stream_decoder;
+int ls_stream_decoder_new(ls_stream_decoder** out);
+void ls_stream_decoder_free(ls_stream_decoder* d);
+int ls_stream_decoder_push(ls_stream_decoder* d, const char* bytes, size_t n, char* out, size_t cap, size_t* len);
+int ls_stream_decoder_finish(ls_stream_decoder* d, char* out, size_t cap, size_t* len);
+
+/* Sampler::new (src/model.rs:309-311) and Sampler::sample (:322-365): greedy at temperature <= 0
+ * (the first maximum), else the top_k largest (at least 1; equal logits by lower index), softmax
+ * at the temperature, the smallest prefix reaching top_p, and a draw from the seeded xorshift64*
+ * stream. logits: n host floats. */
+typedef struct ls_sampler ls_sampler;
+int ls_sampler_new(float temperature, size_t top_k, float top_p, uint64_t seed, ls_sampler** out);
+void ls_sampler_free(ls_sampler* s);
+int ls_sampler_sample(ls_sampler* s, const float* logits, size_t n, uint32_t* token);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,6 +135,22 @@ SIGNATURES = {
     "ls_model_report": (C.c_int, [P, C.POINTER(Report)]),
     "ls_model_last_step_ms": (C.c_double, [P]),
     "ls_model_draft_chain": (C.c_int, [P, C.c_uint32, SZ, U32]),
+    "ls_tokenizer_load": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "ls_tokenizer_free": (None, [P]),
+    "ls_tokenizer_vocab_size": (SZ, [P]),
+    "ls_tokenizer_encode": (C.c_int, [P, C.c_char_p, SZ, U32, SZ, C.POINTER(SZ)]),
+    "ls_tokenizer_decode": (C.c_int, [P, U32, SZ, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "ls_tokenizer_token_bytes": (C.c_int, [P, C.c_uint32, C.c_int, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "ls_tokenizer_token_id": (C.c_int, [P, C.c_char_p, U32]),
+    "ls_tokenizer_is_special": (C.c_int, [P, C.c_uint32]),
+    "ls_tokenizer_pretokens": (C.c_int, [C.c_char_p, SZ, U32, SZ, C.POINTER(SZ)]),
+    "ls_stream_decoder_new": (C.c_int, [C.POINTER(P)]),
+    "ls_stream_decoder_free": (None, [P]),
+    "ls_stream_decoder_push": (C.c_int, [P, C.c_char_p, SZ, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "ls_stream_decoder_finish": (C.c_int, [P, C.c_char_p, SZ, C.POINTER(SZ)]),
+    "ls_sampler_new": (C.c_int, [C.c_float, SZ, C.c_float, C.c_uint64, C.POINTER(P)]),
+    "ls_sampler_free": (None, [P]),
+    "ls_sampler_sample": (C.c_int, [P, F32, SZ, U32]),
     "ls_drafter_from_model": (C.c_int, [P, C.POINTER(Drafter)]),
     "ls_drafter_scripted": (C.c_int, [U32, SZ, C.c_double, C.c_uint64, C.c_uint64, C.POINTER(Drafter)]),
     "ls_drafter_scripted_token": (C.c_uint32, [C.POINTER(Drafter), SZ]),
@@ -597,3 +613,127 @@ def greedy_generate(m: Model, prompt, max_new: int, eos=()):
     n = C.c_size_t(0)
     _check(lib().ls_greedy_generate(m.h, _u32(p), p.size, max_new, _u32(e), len(eos), _u32(out), C.byref(n)))
     return out[: n.value].tolist()
+
+
+def _sized_bytes(call):
+    """Runs call(buf, cap, n_ptr) twice when the first buffer is too small; returns the bytes."""
+    n = C.c_size_t(0)
+    buf = C.create_string_buffer(256)
+    _check(call(buf, 256, C.byref(n)))
+    if n.value > 256:
+        buf = C.create_string_buffer(n.value)
+        _check(call(buf, n.value, C.byref(n)))
+    return buf.raw[: n.value]
+
+
+class Tokenizer:
+    """The Qwen2 byte-level BPE tokenizer (src/tokenizer.rs), in the library (host code)."""
+
+    def __init__(self, model_dir: str):
+        h = C.c_void_p()
+        _check(lib().ls_tokenizer_load(os.fsencode(model_dir), C.byref(h)))
+        self.h = h
+
+    def vocab_size(self) -> int:
+        return lib().ls_tokenizer_vocab_size(self.h)
+
+    def encode(self, text: str) -> list:
+        b = text.encode("utf-8")
+        n = C.c_size_t(0)
+        _check(lib().ls_tokenizer_encode(self.h, b, len(b), None, 0, C.byref(n)))
+        out = np.zeros(max(n.value, 1), np.uint32)
+        _check(lib().ls_tokenizer_encode(self.h, b, len(b), _u32(out), out.size, C.byref(n)))
+        return out[: n.value].tolist()
+
+    def decode(self, ids) -> str:
+        a = _toks(list(ids) or [0])
+        k = len(list(ids))
+        return _sized_bytes(lambda buf, cap, n: lib().ls_tokenizer_decode(self.h, _u32(a), k, buf, cap, n)).decode("utf-8")
+
+    def token_bytes(self, tid: int, show_special: bool = False) -> bytes:
+        return _sized_bytes(lambda buf, cap, n: lib().ls_tokenizer_token_bytes(self.h, tid, int(show_special), buf, cap, n))
+
+    def token_id(self, token: str):
+        i = np.zeros(1, np.uint32)
+        return int(i[0]) if lib().ls_tokenizer_token_id(self.h, token.encode("utf-8"), _u32(i)) else None
+
+    def is_special(self, tid: int) -> bool:
+        return bool(lib().ls_tokenizer_is_special(self.h, tid))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ls_tokenizer_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def pretokens(text: str) -> list:
+    """The pre-token split of text (the Qwen2 pattern), as strings."""
+    b = text.encode("utf-8")
+    n = C.c_size_t(0)
+    _check(lib().ls_tokenizer_pretokens(b, len(b), None, 0, C.byref(n)))
+    ends = np.zeros(max(n.value, 1), np.uint32)
+    _check(lib().ls_tokenizer_pretokens(b, len(b), _u32(ends), ends.size, C.byref(n)))
+    out, start = [], 0
+    for e in ends[: n.value].tolist():
+        out.append(text[start:e])
+        start = e
+    return out
+
+
+class StreamDecoder:
+    """Incremental UTF-8 decoder (src/tokenizer.rs:311-346)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        _check(lib().ls_stream_decoder_new(C.byref(h)))
+        self.h = h
+
+    def push(self, data: bytes) -> str:
+        cap = 3 * (len(data) + 4)
+        buf = C.create_string_buffer(cap)
+        n = C.c_size_t(0)
+        _check(lib().ls_stream_decoder_push(self.h, data, len(data), buf, cap, C.byref(n)))
+        return buf.raw[: n.value].decode("utf-8")
+
+    def finish(self) -> str:
+        buf = C.create_string_buffer(16)
+        n = C.c_size_t(0)
+        _check(lib().ls_stream_decoder_finish(self.h, buf, 16, C.byref(n)))
+        return buf.raw[: n.value].decode("utf-8")
+
+    def __del__(self):
+        try:
+            lib().ls_stream_decoder_free(self.h)
+        except Exception:
+            pass
+
+
+class Sampler:
+    """Sampler (src/model.rs:300-366): greedy at temperature <= 0, else top-k / top-p sampling."""
+
+    def __init__(self, temperature: float, top_k: int, top_p: float, seed: int):
+        h = C.c_void_p()
+        _check(lib().ls_sampler_new(temperature, top_k, top_p, seed, C.byref(h)))
+        self.h = h
+
+    @classmethod
+    def greedy(cls) -> "Sampler":
+        return cls(0.0, 1, 1.0, 0)
+
+    def sample(self, logits) -> int:
+        a = np.ascontiguousarray(np.asarray(logits, np.float32))
+        t = np.zeros(1, np.uint32)
+        _check(lib().ls_sampler_sample(self.h, a.ctypes.data_as(C.POINTER(C.c_float)), a.size, _u32(t)))
+        return int(t[0])
+
+    def __del__(self):
+        try:
+            lib().ls_sampler_free(self.h)
+        except Exception:
+            pass

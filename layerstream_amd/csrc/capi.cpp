@@ -4,9 +4,13 @@
 #include <memory>
 #include <new>
 
+#include <cstring>
+
 #include "model.hpp"
+#include "sampler.hpp"
 #include "spec.hpp"
 #include "static_mm.hpp"
+#include "tokenizer.hpp"
 
 struct ls_source {
     std::unique_ptr<ls::Source> s;
@@ -18,6 +22,18 @@ struct ls_model {
 
 struct ls_spec {
     std::unique_ptr<ls::SpecRun> r;
+};
+
+struct ls_tokenizer {
+    std::unique_ptr<ls::Tokenizer> t;
+};
+
+struct ls_stream_decoder {
+    ls::StreamDecoder d;
+};
+
+struct ls_sampler {
+    std::unique_ptr<ls::Sampler> s;
 };
 
 namespace {
@@ -42,6 +58,19 @@ int guard(F&& f) {
 
 void need(const void* p, const char* what) {
     if (!p) ls::fail(std::string("null ") + what);
+}
+
+// A variable-length result: its size always, the data when it fits.
+template <class T>
+void give(const std::vector<T>& v, T* out, size_t cap, size_t* n) {
+    need(n, "size output");
+    *n = v.size();
+    if (out && cap >= v.size() && !v.empty()) std::memcpy(out, v.data(), v.size() * sizeof(T));
+}
+void give(const std::string& v, char* out, size_t cap, size_t* n) {
+    need(n, "size output");
+    *n = v.size();
+    if (out && cap >= v.size() && !v.empty()) std::memcpy(out, v.data(), v.size());
 }
 
 }  // namespace
@@ -488,6 +517,112 @@ int ls_matmul(ls_format f, const void* w_dev, size_t rows, size_t cols, const fl
         a.ldo = int(rows);
         ls::mm_residual(a, plan, ls::MMScratch{part.as<float>(), cnt.as<int>()}, s);
         HIPC(hipStreamSynchronize(s));
+    });
+}
+
+int ls_tokenizer_load(const char* dir, ls_tokenizer** out) {
+    return guard([&] {
+        need(dir, "directory");
+        need(out, "output");
+        auto t = std::make_unique<ls_tokenizer>();
+        t->t = std::make_unique<ls::Tokenizer>(dir);
+        *out = t.release();
+    });
+}
+
+void ls_tokenizer_free(ls_tokenizer* t) { delete t; }
+
+size_t ls_tokenizer_vocab_size(const ls_tokenizer* t) { return t ? t->t->vocab_size() : 0; }
+
+int ls_tokenizer_encode(const ls_tokenizer* t, const char* text, size_t len, uint32_t* out, size_t cap, size_t* n) {
+    return guard([&] {
+        need(t, "tokenizer");
+        if (len) need(text, "text");
+        give(t->t->encode(std::string(text ? text : "", len)), out, cap, n);
+    });
+}
+
+int ls_tokenizer_decode(const ls_tokenizer* t, const uint32_t* ids, size_t n, char* out, size_t cap, size_t* len) {
+    return guard([&] {
+        need(t, "tokenizer");
+        if (n) need(ids, "ids");
+        give(t->t->decode(ids, n), out, cap, len);
+    });
+}
+
+int ls_tokenizer_token_bytes(const ls_tokenizer* t, uint32_t id, int show_special, char* out, size_t cap, size_t* len) {
+    return guard([&] {
+        need(t, "tokenizer");
+        give(t->t->token_bytes(id, show_special != 0), out, cap, len);
+    });
+}
+
+int ls_tokenizer_token_id(const ls_tokenizer* t, const char* token, uint32_t* id) {
+    if (!t || !token || !id) return 0;
+    return t->t->token_id(token, id) ? 1 : 0;
+}
+
+int ls_tokenizer_is_special(const ls_tokenizer* t, uint32_t id) { return t && t->t->is_special(id) ? 1 : 0; }
+
+int ls_tokenizer_pretokens(const char* text, size_t len, uint32_t* ends, size_t cap, size_t* n) {
+    return guard([&] {
+        if (len) need(text, "text");
+        const std::vector<uint32_t> cps = ls::utf8_to_cps(std::string(text ? text : "", len));
+        std::vector<uint32_t> e;
+        for (size_t i = 0; i < cps.size();) {
+            i = ls::Tokenizer::pretoken_end(cps, i);
+            e.push_back(uint32_t(i));
+        }
+        give(e, ends, cap, n);
+    });
+}
+
+int ls_stream_decoder_new(ls_stream_decoder** out) {
+    return guard([&] {
+        need(out, "output");
+        *out = new ls_stream_decoder();
+    });
+}
+
+void ls_stream_decoder_free(ls_stream_decoder* d) { delete d; }
+
+int ls_stream_decoder_push(ls_stream_decoder* d, const char* bytes, size_t n, char* out, size_t cap, size_t* len) {
+    return guard([&] {
+        need(d, "decoder");
+        need(out, "output");
+        if (n) need(bytes, "bytes");
+        if (cap < 3 * (n + 4)) ls::fail("the output buffer must hold 3 * (n + 4) bytes");
+        give(d->d.push(std::string(bytes ? bytes : "", n)), out, cap, len);
+    });
+}
+
+int ls_stream_decoder_finish(ls_stream_decoder* d, char* out, size_t cap, size_t* len) {
+    return guard([&] {
+        need(d, "decoder");
+        need(out, "output");
+        if (cap < 12) ls::fail("the output buffer must hold 12 bytes");
+        give(d->d.finish(), out, cap, len);
+    });
+}
+
+int ls_sampler_new(float temperature, size_t top_k, float top_p, uint64_t seed, ls_sampler** out) {
+    return guard([&] {
+        need(out, "output");
+        auto s = std::make_unique<ls_sampler>();
+        s->s = std::make_unique<ls::Sampler>(temperature, top_k, top_p, seed);
+        *out = s.release();
+    });
+}
+
+void ls_sampler_free(ls_sampler* s) { delete s; }
+
+int ls_sampler_sample(ls_sampler* s, const float* logits, size_t n, uint32_t* token) {
+    return guard([&] {
+        need(s, "sampler");
+        need(token, "token");
+        if (n == 0) ls::fail("no logits to sample from");
+        need(logits, "logits");
+        *token = s->s->sample(logits, n);
     });
 }
 

@@ -388,6 +388,77 @@ uint32_t or_argmax(const float* v, size_t n) {
 }
 
 /* ---------------------------------------------------------------------------------------
+ * Sampler: src/model.rs:300-366
+ * ------------------------------------------------------------------------------------- */
+/* Sampler::new (:309-311): top_k at least 1, state seed * 0x9E3779B97F4A7C15 | 1. */
+void or_sampler_init(or_sampler* s, float temperature, size_t top_k, float top_p, uint64_t seed) {
+    s->temperature = temperature;
+    s->top_k = top_k < 1 ? 1 : top_k;
+    s->top_p = top_p;
+    s->state = (seed * 0x9E3779B97F4A7C15ull) | 1;
+}
+
+/* Sampler::next_uniform (:317-324): xorshift64*, (r >> 40) / 2^24 in f32. */
+float or_sampler_uniform(or_sampler* s) {
+    s->state ^= s->state >> 12;
+    s->state ^= s->state << 25;
+    s->state ^= s->state >> 27;
+    uint64_t r = s->state * 0x2545F4914F6CDD1Dull;
+    return (float)(uint32_t)(r >> 40) / (float)(1u << 24);
+}
+
+static const float* g_sort_logits;
+/* descending logit; equal logits keep index order (the reference's selection leaves their order
+ * unspecified) */
+static int desc_logit(const void* a, const void* b) {
+    uint32_t i = *(const uint32_t*)a, j = *(const uint32_t*)b;
+    float x = g_sort_logits[i], y = g_sort_logits[j];
+    if (x > y) return -1;
+    if (x < y) return 1;
+    return i < j ? -1 : (i > j ? 1 : 0);
+}
+
+/* Sampler::sample (:326-365). */
+uint32_t or_sampler_sample(or_sampler* s, const float* logits, size_t n) {
+    if (s->temperature <= 0.0f) return or_argmax(logits, n);
+    size_t k = s->top_k < n ? s->top_k : n;
+    uint32_t* idx = (uint32_t*)malloc(n * sizeof(uint32_t));
+    float* probs = (float*)malloc(k * sizeof(float));
+    for (size_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
+    g_sort_logits = logits;
+    qsort(idx, n, sizeof(uint32_t), desc_logit);
+    float max = logits[idx[0]];
+    for (size_t i = 0; i < k; i++) probs[i] = expf((logits[idx[i]] - max) / s->temperature);
+    float sum = 0.0f;
+    for (size_t i = 0; i < k; i++) sum += probs[i];
+    for (size_t i = 0; i < k; i++) probs[i] /= sum;
+    /* nucleus cut */
+    float cum = 0.0f;
+    size_t keep = k;
+    for (size_t i = 0; i < k; i++) {
+        cum += probs[i];
+        if (cum >= s->top_p) {
+            keep = i + 1;
+            break;
+        }
+    }
+    float total = 0.0f;
+    for (size_t i = 0; i < keep; i++) total += probs[i];
+    float r = or_sampler_uniform(s) * total;
+    uint32_t out = idx[keep - 1];
+    for (size_t i = 0; i < keep; i++) {
+        r -= probs[i];
+        if (r <= 0.0f) {
+            out = idx[i];
+            break;
+        }
+    }
+    free(idx);
+    free(probs);
+    return out;
+}
+
+/* ---------------------------------------------------------------------------------------
  * Quantizer: src/quant.rs:35-145, 158-251
  * ------------------------------------------------------------------------------------- */
 static const float CLIPS[9] = {1.0f, 0.95f, 0.9f, 0.85f, 0.8f, 0.75f, 0.7f, 0.65f, 0.6f};

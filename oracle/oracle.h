@@ -57,6 +57,16 @@ void or_rope_inplace(float* head, const float* inv_freq, size_t hd, size_t pos);
 void or_softmax_inplace(float* v, size_t n);                                                            /* :254-265 */
 float or_silu(float x);                                                                                 /* :268-270 */
 uint32_t or_argmax(const float* v, size_t n);                                                           /* src/spec.rs:41-49 */
+/* Sampler (src/model.rs:300-366). */
+typedef struct {
+    float temperature;
+    size_t top_k;
+    float top_p;
+    uint64_t state;
+} or_sampler;
+void or_sampler_init(or_sampler* s, float temperature, size_t top_k, float top_p, uint64_t seed);
+float or_sampler_uniform(or_sampler* s);
+uint32_t or_sampler_sample(or_sampler* s, const float* logits, size_t n);
 
 /* ---- pool (src/pool.rs) and matmul (src/kernels.rs:123-203) ---- */
 typedef struct or_pool or_pool;

@@ -48,6 +48,25 @@ class SpecStats(C.Structure):
     ]
 
 
+class OrSampler(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_size_t), ("top_p", C.c_float), ("state", C.c_uint64)]
+
+
+class Sampler:
+    """The oracle's Sampler (src/model.rs:300-366)."""
+
+    def __init__(self, temperature: float, top_k: int, top_p: float, seed: int):
+        self.s = OrSampler()
+        lib().or_sampler_init(C.byref(self.s), temperature, top_k, top_p, seed)
+
+    def uniform(self) -> float:
+        return lib().or_sampler_uniform(C.byref(self.s))
+
+    def sample(self, logits) -> int:
+        a = np.ascontiguousarray(np.asarray(logits, np.float32))
+        return int(lib().or_sampler_sample(C.byref(self.s), f32(a), a.size))
+
+
 class Drafter(C.Structure):
     _fields_ = [
         ("model", C.c_void_p),
@@ -91,6 +110,9 @@ def lib():
             "or_softmax_inplace": (None, [F32, SZ]),
             "or_silu": (C.c_float, [C.c_float]),
             "or_argmax": (C.c_uint32, [F32, SZ]),
+            "or_sampler_init": (None, [C.POINTER(OrSampler), C.c_float, SZ, C.c_float, C.c_uint64]),
+            "or_sampler_uniform": (C.c_float, [C.POINTER(OrSampler)]),
+            "or_sampler_sample": (C.c_uint32, [C.POINTER(OrSampler), F32, SZ]),
             "or_pool_new": (P, [C.c_int]),
             "or_pool_free": (None, [P]),
             "or_matmul": (None, [P, Fmt, U8, SZ, SZ, F32, SZ, F32]),
