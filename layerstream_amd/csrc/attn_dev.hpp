@@ -234,6 +234,12 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     const int last_key = pos_first + nq - 1;
     const int nb = last_key / AKB + 1;
     const int first = s * AWV + w, stride = ASPLIT * AWV;
+    // Splits whose first block is past the last key hold nothing: their state would be
+    // (-inf, 0, 0), which the final merge adds exactly nothing from. In a launch of its own
+    // (no flows) such a workgroup leaves at once and the merge counts only the live ones.
+    constexpr bool SKIP = !OUT_FLOW && !IN_FLOW;
+    const int live = SKIP ? min(ASPLIT, (nb + AWV - 1) / AWV) : ASPLIT;
+    if (SKIP && s >= live) return;
     const size_t rows_total = size_t(t) * heads;
     const __amdgpu_buffer_rsrc_t rm = coherent_rsrc(pm, rows_total * ASPLIT * 4);
     const __amdgpu_buffer_rsrc_t rl = coherent_rsrc(pl, rows_total * ASPLIT * 4);
@@ -369,7 +375,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
     if (tid == 0) {
         int* cn = A.cnt + size_t(seg) * heads + head;
         const int old = __hip_atomic_fetch_add(cn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == ASPLIT - 1;
+        const int last = old == live - 1;
         if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         flag = last;
     }
@@ -383,6 +389,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         float mv[ASPLIT], lv[ASPLIT], ov[ASPLIT][DPT];
 #pragma unroll
         for (int k = 0; k < ASPLIT; k++) {
+            if (k >= live) {  // a split that held no keys: the state it would have stored
+                mv[k] = -INFINITY;
+                lv[k] = 0.0f;
+#pragma unroll
+                for (int u = 0; u < DPT; u++) ov[k][u] = 0.0f;
+                continue;
+            }
             mv[k] = ld_f32(rm, int((base + k) * 4));
             lv[k] = ld_f32(rl, int((base + k) * 4));
             if constexpr (DPT % 4 == 0) {
@@ -425,6 +438,252 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         else write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
     }
     if constexpr (OUT_FLOW) flow_signal(fl, 0);
+}
+
+// ---------------------------------------------------------------------------------------
+// The same attention with the query heads of a KV group together (launches over several token
+// tiles or a batch's segments): workgroup (s, group, segment) takes split s of every head of the
+// group. A wavefront loads its key block's K and V once (when it holds one block, as every
+// wavefront does up to 1024 keys) and runs each head's MFMAs on them, the next head's q loaded
+// while the current head is computed; each head's state is merged over the wavefronts in LDS and
+// stored, and the last of the ASPLIT workgroups of (group, segment) merges every head of the
+// group. Per head this is attn_body's arithmetic in attn_body's order (the same blocks per
+// wavefront, the same two merges), so the bits do not change; the launch has heads / kv_heads
+// times fewer workgroups and reads the cache that many times less.
+// ---------------------------------------------------------------------------------------
+// LDS of a grouped workgroup: attn_body's, then the q rows of up to AWV heads [head][16][HD].
+template <int HD>
+__host__ __device__ constexpr size_t attn_grp_lds_bytes() { return attn_lds_bytes<HD>() + size_t(AWV) * ATQ * HD * 4; }
+
+template <int HD>
+__device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int grp, int seg, uint8_t* smem) {
+    const float* __restrict__ q = A.q;
+    const int ldq = A.ldq, t = A.t, heads = A.heads, kv_heads = A.kv_heads, hpg = heads / kv_heads;
+    const AttnRows& rows = A.rows;
+    const float scale = A.scale;
+    const float* __restrict__ kc = A.kc;
+    const float* __restrict__ vc = A.vc;
+    uint8_t* __restrict__ frags = A.frags;
+    const size_t frag_stride = A.frag_stride;
+    constexpr int H4 = HD / 4, DB = HD / 16;
+    float(*sm_m)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem);
+    float(*sm_l)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem + AWV * ATQ * 4);
+    constexpr int HP = HD + 4;
+    float* sm_o = reinterpret_cast<float*>(smem + 2 * AWV * ATQ * 4);
+    int& flag = *reinterpret_cast<int*>(smem + 2 * AWV * ATQ * 4 + AWV * ATQ * HP * 4);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
+    const int kv = kv_heads * HD, col0 = grp * HD;
+    int i0, nq, pos_first;
+    if (rows.segs) {
+        const int4 sg = rows.segs[seg];
+        i0 = sg.x;
+        nq = sg.y;
+        pos_first = rows.pos[i0];
+        kc += size_t(sg.z) * rows.seq_stride;
+        vc += size_t(sg.z) * rows.seq_stride;
+    } else {
+        i0 = seg * ATQ;
+        nq = min(ATQ, t - i0);
+        pos_first = *A.pos0p + i0;
+    }
+    const int tile = i0 / ATQ, tok0 = i0 % ATQ;
+    const int last_key = pos_first + nq - 1;
+    const int nb = last_key / AKB + 1;
+    const int first = s * AWV + w, stride = ASPLIT * AWV;
+    const int live = min(ASPLIT, (nb + AWV - 1) / AWV);  // splits that hold keys (as attn_body)
+    if (s >= live) return;
+    const bool one_block = first < nb && first + stride >= nb;  // this wavefront's only block: loaded once
+    const size_t rows_total = size_t(t) * heads;
+    const __amdgpu_buffer_rsrc_t rm = coherent_rsrc(A.pm, rows_total * ASPLIT * 4);
+    const __amdgpu_buffer_rsrc_t rl = coherent_rsrc(A.pl, rows_total * ASPLIT * 4);
+    const __amdgpu_buffer_rsrc_t ro = coherent_rsrc(A.po, rows_total * ASPLIT * HD * 4);
+
+    AttnBlock<HD> ba;
+    if (one_block) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
+    // Every head's q rows into LDS at once (rows past nq: zeros).
+    float* sq = reinterpret_cast<float*>(smem + attn_lds_bytes<HD>());
+    for (int e = tid; e < hpg * ATQ * (HD / 4); e += AWV * 64) {
+        const int hh = e / (ATQ * (HD / 4)), tk = (e / (HD / 4)) % ATQ, d = 4 * (e % (HD / 4));
+        const float4 x = tk < nq ? *reinterpret_cast<const float4*>(q + size_t(i0 + tk) * ldq + (grp * hpg + hh) * HD + d)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        *reinterpret_cast<float4*>(sq + (hh * ATQ + tk) * HD + d) = x;
+    }
+    __syncthreads();
+    float qr[H4];
+    for (int hh = 0; hh < hpg; hh++) {
+        const int head = grp * hpg + hh;
+#pragma unroll
+        for (int j = 0; j < H4; j += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(sq + (hh * ATQ + c) * HD + g * H4 + j);
+            qr[j] = x.x;
+            qr[j + 1] = x.y;
+            qr[j + 2] = x.z;
+            qr[j + 3] = x.w;
+        }
+        float M = -INFINITY, Lp = 0.0f;
+        attn_f32x4 O[DB];
+#pragma unroll
+        for (int db = 0; db < DB; db++) O[db] = attn_f32x4{0, 0, 0, 0};
+        auto block = [&](int b, const AttnBlock<HD>& r) {
+            attn_f32x4 sc = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < H4; j++) sc = mfma_f32(r.k[j], qr[j], sc);
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = AKB * b + 4 * g + i;
+                sv[i] = (c < nq && key <= pos_first + c) ? sc[i] * scale : -INFINITY;
+                mx = fmaxf(mx, sv[i]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float Mn = fmaxf(M, mx);
+            const float corr = M == -INFINITY ? 0.0f : expf(M - Mn);
+            float p[4], ls = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
+                ls += p[i];
+            }
+            Lp = __builtin_fmaf(Lp, corr, ls);
+            M = Mn;
+#pragma unroll
+            for (int db = 0; db < DB; db++) {
+                attn_f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < 4; u++) acc = mfma_f32(r.v[u * DB + db], p[u], acc);
+#pragma unroll
+                for (int i = 0; i < 4; i++) O[db][i] = __builtin_fmaf(O[db][i], corr, acc[i]);
+            }
+        };
+        if (one_block) {
+            block(first, ba);
+        } else {
+            for (int b = first; b < nb; b += stride) {
+                AttnBlock<HD> r;
+                attn_load<HD>(r, b, last_key, kc, vc, kv, col0, g, c);
+                block(b, r);
+            }
+        }
+        // The wavefronts' states of this head, merged in wavefront order (as attn_body).
+        float L = Lp + __shfl_xor(Lp, 16, 64);
+        L += __shfl_xor(L, 32, 64);
+        if (g == 0) {
+            sm_m[w][c] = M;
+            sm_l[w][c] = L;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float* dst = &sm_o[(w * ATQ + c) * HP + DB * (4 * g + i)];
+            if constexpr (DB % 4 == 0) {
+#pragma unroll
+                for (int db = 0; db < DB; db += 4)
+                    *reinterpret_cast<attn_f32x4*>(dst + db) = attn_f32x4{O[db][i], O[db + 1][i], O[db + 2][i], O[db + 3][i]};
+            } else {
+#pragma unroll
+                for (int db = 0; db < DB; db++) dst[db] = O[db][i];
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < ATQ * (HD / 4); e += AWV * 64) {
+            const int tk = e % ATQ, d = 4 * (e / ATQ);
+            if (tk >= nq) continue;
+            float mw[AWV], Mx = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < AWV; k++) {
+                mw[k] = sm_m[k][tk];
+                Mx = fmaxf(Mx, mw[k]);
+            }
+            float Lw = 0.0f;
+            attn_f32x4 ow = {0, 0, 0, 0};
+#pragma unroll
+            for (int k = 0; k < AWV; k++) {
+                const float e2 = mw[k] == -INFINITY ? 0.0f : expf(mw[k] - Mx);
+                Lw = __builtin_fmaf(sm_l[k][tk], e2, Lw);
+                const attn_f32x4 x = *reinterpret_cast<const attn_f32x4*>(&sm_o[(k * ATQ + tk) * HP + d]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) ow[i] = __builtin_fmaf(x[i], e2, ow[i]);
+            }
+            const size_t row = (size_t(i0 + tk) * heads + head) * ASPLIT + s;
+            if (d == 0) {
+                st_f32(Mx, rm, int(row * 4));
+                st_f32(Lw, rl, int(row * 4));
+            }
+            st_attn_f32x4(ow, ro, int((row * HD + d) * 4));
+        }
+        __syncthreads();  // before the next head reuses the LDS
+    }
+
+    // The last workgroup of (group, segment) merges the ASPLIT states of every head in order.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        int* cn = A.cnt + size_t(seg) * kv_heads + grp;
+        const int old = __hip_atomic_fetch_add(cn, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == live - 1;
+        if (last) __hip_atomic_store(cn, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flag = last;
+    }
+    __syncthreads();
+    if (!flag) return;
+    // (head, token) pairs over the 32 row slots of the workgroup, every head's rows into LDS
+    // ([pair][HD]: at most heads_per_group x 16 rows), then the fragments.
+    constexpr int DPT = HD / 16;
+    float* Os = sm_o;
+    const int sub = tid & 15;
+    for (int pr = tid >> 4; pr < hpg * nq; pr += AWV * 64 / 16) {
+        const int hh = pr / nq, row = pr % nq, head = grp * hpg + hh;
+        const size_t base = (size_t(i0 + row) * heads + head) * ASPLIT;
+        float mv[ASPLIT], lv[ASPLIT], ov[ASPLIT][DPT];
+#pragma unroll
+        for (int k = 0; k < ASPLIT; k++) {
+            if (k >= live) {
+                mv[k] = -INFINITY;
+                lv[k] = 0.0f;
+#pragma unroll
+                for (int u = 0; u < DPT; u++) ov[k][u] = 0.0f;
+                continue;
+            }
+            mv[k] = ld_f32(rm, int((base + k) * 4));
+            lv[k] = ld_f32(rl, int((base + k) * 4));
+            if constexpr (DPT % 4 == 0) {
+#pragma unroll
+                for (int u = 0; u < DPT; u += 4) {
+                    const attn_f32x4 x = ld_attn_f32x4(ro, int(((base + k) * HD + sub * DPT + u) * 4));
+                    ov[k][u] = x[0];
+                    ov[k][u + 1] = x[1];
+                    ov[k][u + 2] = x[2];
+                    ov[k][u + 3] = x[3];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < DPT; u++) ov[k][u] = ld_f32(ro, int(((base + k) * HD + sub * DPT + u) * 4));
+            }
+        }
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < ASPLIT; k++) Mx = fmaxf(Mx, mv[k]);
+        float Lt = 0.0f, o[DPT];
+#pragma unroll
+        for (int u = 0; u < DPT; u++) o[u] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ASPLIT; k++) {
+            const float e = mv[k] == -INFINITY ? 0.0f : expf(mv[k] - Mx);
+            Lt = __builtin_fmaf(lv[k], e, Lt);
+#pragma unroll
+            for (int u = 0; u < DPT; u++) o[u] = __builtin_fmaf(ov[k][u], e, o[u]);
+        }
+        const float inv = 1.0f / Lt;
+#pragma unroll
+        for (int u = 0; u < DPT; u++) Os[pr * HD + sub * DPT + u] = o[u] * inv;
+    }
+    __syncthreads();
+    uint8_t* tf = frags + size_t(tile) * frag_stride;
+    for (int p = tid; p < hpg * nq * (HD / 8); p += AWV * 64) {
+        const int pr = p / (HD / 8), sl = p % (HD / 8), hh = pr / nq, i = pr % nq, col = (grp * hpg + hh) * HD + 8 * sl;
+        write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + pr * HD + 8 * sl);
+    }
 }
 
 }  // namespace ls

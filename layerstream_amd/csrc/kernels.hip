@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -28,14 +29,35 @@ __global__ __launch_bounds__(AWV * 64) void k_attn(AttnArgs a) {
     attn_body<HD, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, Flow{}, smem);
 }
 
+template <int HD>
+__global__ __launch_bounds__(AWV * 64, HD <= 64 ? 4 : 2) void k_attn_grp(AttnArgs a) {  // head_dim <= 64: two workgroups per CU
+    __shared__ __align__(16) uint8_t smem[attn_grp_lds_bytes<HD>()];
+    attn_group_body<HD>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+}
+
 size_t attention_scratch_floats(int t, int heads, int hd, int) { return size_t(t) * heads * ASPLIT * (hd + 2); }
+
+// A batch's segments run with the heads of a KV group together (k_attn_grp) unless
+// LS_ATTN_GROUP=0 (one workgroup per head and split, k_attn; token tiles of one sequence always
+// do): the same bits either way.
+static bool attn_grouped() {
+    static const bool on = [] {
+        const char* e = std::getenv("LS_ATTN_GROUP");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
 
 template <int HD>
 static void launch_attn(const float* q, int ldq, int t, int heads, int kv_heads, const int* pos0, const AttnRows& rows,
                         const float* kc, const float* vc, float* scratch, int* cnt, uint8_t* frags, hipStream_t s) {
     const AttnArgs a = make_attn_args(q, ldq, t, heads, kv_heads, HD, pos0, rows, kc, vc, scratch, cnt, frags);
     const int nseg = rows.segs ? rows.n_segs : (t + ATQ - 1) / ATQ;
-    hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(AWV * 64), 0, s, a);
+    // (the final merge holds a group's output rows in the LDS of the wavefront outputs)
+    if (attn_grouped() && rows.segs && heads > kv_heads && heads / kv_heads <= AWV)
+        hipLaunchKernelGGL(k_attn_grp<HD>, dim3(ASPLIT, kv_heads, nseg), dim3(AWV * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_attn<HD>, dim3(ASPLIT, heads, nseg), dim3(AWV * 64), 0, s, a);
     HIPCHECK(hipGetLastError());
 }
 
