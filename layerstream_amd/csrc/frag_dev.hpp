@@ -13,6 +13,8 @@ namespace ls {
 // Cache policy of data handed between workgroups of one launch: sc1, coherent across the L2s
 // of the XCDs.
 constexpr int CPOL_SC1 = 16;
+// Cache policy of data read once (weights): nt, streamed past the caches.
+constexpr int CPOL_NT = 2;
 constexpr int BUF_DWORD3 = 0x00020000;  // raw buffer resource word 3 on gfx9
 
 // f32 value -> three bf16 terms (truncations) whose sum is the value exactly.

@@ -211,6 +211,12 @@ void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStrea
 // gate|up projection (row blocks of 16 GU_STRIPS interleaved gate, up; plan from gu_plan) +
 // 1/rms + SiLU(g) * u -> act fragments.
 void mm_gate_up(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s);
+// The same gate|up over one token tile as a pipelined launch (one workgroup per CU walking a range
+// of gate and up strip pairs, its input fragments held in registers, the next pairs' weights in
+// flight while one pair's epilogue runs); the same bits as mm_gate_up under the same plan. Fits a
+// plan of one tile, one row group, 16 wavefronts along K, no K split, scale groups inside a chunk.
+bool mm_gate_up_pipe_fits(const MMArgs& a, const MMPlan& p);
+void mm_gate_up_pipe(const MMArgs& a, const MMPlan& p, hipStream_t s);
 // gate|up then down (plan strips DOWN_STRIPS) in one launch for one token tile: each down K
 // split waits only for the gate|up row blocks that produce its columns. ctl is the control
 // block (FLOW_WORDS ints).

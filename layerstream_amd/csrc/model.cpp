@@ -698,6 +698,7 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
     if (const char* e = std::getenv("LS_PF")) pf_on_ = std::atoi(e) != 0;  // weight prefetch in fused launches (default on)
     if (const char* e = std::getenv("LS_STACK")) stack_on_ = std::atoi(e) != 0;  // layer-stack launch (default on)
+    if (const char* e = std::getenv("LS_PIPE")) pipe_on_ = std::atoi(e) != 0;  // pipelined large gate|up (default on)
     if (const char* e = std::getenv("LS_DIRECT")) direct_on_ = std::atoi(e) != 0;  // verify staging without copies (default on)
     if (const char* e = std::getenv("LS_STEP_EVENTS")) step_events_ = std::atoi(e) != 0;  // device events around each step (default off)
     x_ = DevBuf(T * h * 4);
@@ -1148,8 +1149,10 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 prof_end(L.gu, T);
                 prof_end(L.down, T, false);
             } else {
+                // gate|up with more strip pairs than CUs: the pipelined launch (same bits).
                 prof_begin();
-                mm_gate_up(g, pg, scr, s);
+                if (pipe_on_ && mm_gate_up_pipe_fits(g, pg) && pg.nrb * GU_STRIPS > device_cu_count()) mm_gate_up_pipe(g, pg, s);
+                else mm_gate_up(g, pg, scr, s);
                 prof_end(L.gu, T);
                 prof_begin();
                 mm_residual(d, pd, scr, s);

@@ -207,6 +207,7 @@ private:
     bool fuse_on_ = true;
     bool fuse_qkv_ = true;  // q|k|v joins the attention + o launch
     bool pf_on_ = true;     // fused consumers prefetch the next launch's weights
+    bool pipe_on_ = true;   // large single-tile gate|up as a pipelined launch (LS_PIPE=0: k_mm)
     bool stack_on_ = true;  // one-tile passes over resident layers run as one layer-stack launch (LS_STACK=0: per layer)
     const int* stage_pos_ = nullptr;  // device positions of the staged chunks
     size_t vpad_ = 0, fb_h_ = 0, fb_q_ = 0, fb_in_ = 0;

@@ -519,6 +519,30 @@ def test_qwen3b_int8_verify_step_matches_the_oracle():
     verify_step_vs_oracle(m, prompt, 8, rng, 256, "3B int8:")
 
 
+def test_qwen3b_pipelined_matrices_give_the_bits_of_k_mm():
+    """Over one token tile the 3B gate|up (688 gate and up strip pairs) has more strip pairs than
+    the device has CUs and runs as the pipelined launch; LS_PIPE=0 runs it as k_mm. Same plan, so
+    the same logits bit for bit and the same acceptance, over blocks of 9, 1 and 9 tokens in a row
+    (the first 40-token prompt runs k_mm over three tiles either way)."""
+    say("3B pipelined vs k_mm: build")
+    m = qwen3b((8, 64))
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, 151936, 40).tolist()
+    with env("LS_PIPE", "0"):
+        a = gpu_model(m, max_ctx=256)
+    b = gpu_model(m, max_ctx=256)
+    assert np.array_equal(bits(a.forward(prompt)), bits(b.forward(prompt)))
+    for block in ([8, 9, 400, 33, 120, 5, 77, 301, 2], [17], [3, 4, 5, 6, 7, 8, 9, 10, 11]):
+        say("3B pipelined vs k_mm: block of", len(block))
+        p = a.pos()
+        va, vb = a.forward_multi(block, len(block)), b.forward_multi(block, len(block))
+        assert np.array_equal(bits(va), bits(vb)), len(block)
+        a.truncate(p)
+        b.truncate(p)
+        assert a.verify_greedy(block) == b.verify_greedy(block), len(block)
+        assert a.pos() == b.pos()
+
+
 def test_qwen05b_int4_verify_step_after_a_long_prompt_matches_the_oracle():
     """The int4-g32 configuration's shape with a 1100-token prompt (nine prefill chunks; the
     verify rows attend over 69 blocks of 16 keys), one verify step of k=8."""
