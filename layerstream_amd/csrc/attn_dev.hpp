@@ -19,8 +19,9 @@ namespace ls {
 // cached position.
 //
 // One launch: grid (ASPLIT, heads, row segments) of AWV-wavefront workgroups. A segment is a run
-// of at most 16 consecutive rows of one sequence inside one 16-row tile: every token tile of a
-// single sequence, or the pieces of a batch of sequences cut at tile boundaries. The keys are
+// of at most 16 consecutive rows of one sequence: every token tile of a single sequence, or, in a
+// batch, a sequence's rows in pieces of 16 from its first row (a piece may straddle two tiles; each
+// row's output goes to its own tile). A row's result depends only on its own query and keys. The keys are
 // cut into 16-key blocks; block b belongs to wavefront b % (AWV ASPLIT) of the (head, segment)
 // (workgroup (b % (AWV ASPLIT)) / AWV), which keeps a running (max, sum, output) per token over its
 // blocks in order (online softmax) without any barrier: the scores ([keys][tokens]) and the
@@ -430,28 +431,35 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         for (int u = 0; u < DPT; u++) Os[row * HD + sub * DPT + u] = o[u] * inv;
     }
     __syncthreads();
+    // Row i0 + i goes to token (i0 + i) % 16 of tile (i0 + i) / 16 (a batch segment may straddle
+    // two tiles; launches with in-launch consumers run whole tiles).
     uint8_t* tf = frags + size_t(tile) * frag_stride;
     const __amdgpu_buffer_rsrc_t rf = __builtin_amdgcn_make_buffer_rsrc(tf, 0, int(frag_stride), BUF_DWORD3);
     for (int p = tid; p < nq * (HD / 8); p += AWV * 64) {
         const int i = p / (HD / 8), sl = p % (HD / 8), col = head * HD + 8 * sl;
-        if constexpr (OUT_FLOW) write_slot_coherent(rf, 0, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
-        else write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
+        if constexpr (OUT_FLOW) {
+            write_slot_coherent(rf, 0, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
+        } else {
+            const int r = i0 + i;
+            write_slot(frags + size_t(r / ATQ) * frag_stride, col / 32, r % ATQ + 16 * ((col % 32) / 8), Os + i * HD + 8 * sl);
+        }
     }
     if constexpr (OUT_FLOW) flow_signal(fl, 0);
 }
 
 // ---------------------------------------------------------------------------------------
-// The same attention with the query heads of a KV group together (launches over several token
-// tiles or a batch's segments): workgroup (s, group, segment) takes split s of every head of the
-// group. A wavefront loads its key block's K and V once (when it holds one block, as every
-// wavefront does up to 1024 keys) and runs each head's MFMAs on them, the next head's q loaded
-// while the current head is computed; each head's state is merged over the wavefronts in LDS and
-// stored, and the last of the ASPLIT workgroups of (group, segment) merges every head of the
-// group. Per head this is attn_body's arithmetic in attn_body's order (the same blocks per
-// wavefront, the same two merges), so the bits do not change; the launch has heads / kv_heads
-// times fewer workgroups and reads the cache that many times less.
+// The same attention with the query heads of a KV group together (a batch's segments): workgroup
+// (s, group, segment) takes split s of every head of the group. A wavefront loads its key block's
+// K and V once (when it holds one block, as every wavefront does up to 1024 keys) and runs them
+// against the group's (head, row) pairs, 16 pairs per MFMA query tile (a 9-row verify block of 7
+// heads fills 4 tiles where a head at a time would take 7 of 9 live columns); each tile's states
+// are merged over the wavefronts in LDS and stored, and the last of the ASPLIT workgroups of
+// (group, segment) merges every pair. Per (head, row) this is attn_body's arithmetic in
+// attn_body's order (the same blocks per wavefront, the same two merges; a query column's results
+// depend only on its own q), so the bits do not change; the launch has heads / kv_heads times
+// fewer workgroups and reads the cache that many times less.
 // ---------------------------------------------------------------------------------------
-// LDS of a grouped workgroup: attn_body's, then the q rows of up to AWV heads [head][16][HD].
+// LDS of a grouped workgroup: attn_body's, then the q of up to AWV x 16 (head, row) pairs [pair][HD].
 template <int HD>
 __host__ __device__ constexpr size_t attn_grp_lds_bytes() { return attn_lds_bytes<HD>() + size_t(AWV) * ATQ * HD * 4; }
 
@@ -486,7 +494,6 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
         nq = min(ATQ, t - i0);
         pos_first = *A.pos0p + i0;
     }
-    const int tile = i0 / ATQ, tok0 = i0 % ATQ;
     const int last_key = pos_first + nq - 1;
     const int nb = last_key / AKB + 1;
     const int first = s * AWV + w, stride = ASPLIT * AWV;
@@ -500,21 +507,27 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
 
     AttnBlock<HD> ba;
     if (one_block) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
-    // Every head's q rows into LDS at once (rows past nq: zeros).
+    // The group's (head, row) pairs, pair hh nq + i = head grp hpg + hh at row i0 + i, fill the
+    // 16 query columns of the MFMAs in tiles of 16 (9-row verify blocks of 7 heads: 4 tiles of
+    // 16, not 7 of 9). Every pair's q into LDS at once (slots past the pairs: zeros).
     float* sq = reinterpret_cast<float*>(smem + attn_lds_bytes<HD>());
-    for (int e = tid; e < hpg * ATQ * (HD / 4); e += AWV * 64) {
-        const int hh = e / (ATQ * (HD / 4)), tk = (e / (HD / 4)) % ATQ, d = 4 * (e % (HD / 4));
-        const float4 x = tk < nq ? *reinterpret_cast<const float4*>(q + size_t(i0 + tk) * ldq + (grp * hpg + hh) * HD + d)
-                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        *reinterpret_cast<float4*>(sq + (hh * ATQ + tk) * HD + d) = x;
+    const int npairs = hpg * nq, ptiles = (npairs + ATQ - 1) / ATQ;
+    for (int e = tid; e < ptiles * ATQ * (HD / 4); e += AWV * 64) {
+        const int pr = e / (HD / 4), d = 4 * (e % (HD / 4));
+        float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (pr < npairs) x = *reinterpret_cast<const float4*>(q + size_t(i0 + pr % nq) * ldq + (grp * hpg + pr / nq) * HD + d);
+        *reinterpret_cast<float4*>(sq + pr * HD + d) = x;
     }
     __syncthreads();
     float qr[H4];
-    for (int hh = 0; hh < hpg; hh++) {
-        const int head = grp * hpg + hh;
+    for (int pt = 0; pt < ptiles; pt++) {
+        // Query column c: pair pt 16 + c, its row at position pos_first + row.
+        const int pc = pt * ATQ + c;
+        const bool live_c = pc < npairs;
+        const int pos_c = pos_first + pc % nq;
 #pragma unroll
         for (int j = 0; j < H4; j += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(sq + (hh * ATQ + c) * HD + g * H4 + j);
+            const float4 x = *reinterpret_cast<const float4*>(sq + pc * HD + g * H4 + j);
             qr[j] = x.x;
             qr[j + 1] = x.y;
             qr[j + 2] = x.z;
@@ -533,7 +546,7 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int key = AKB * b + 4 * g + i;
-                sv[i] = (c < nq && key <= pos_first + c) ? sc[i] * scale : -INFINITY;
+                sv[i] = (live_c && key <= pos_c) ? sc[i] * scale : -INFINITY;
                 mx = fmaxf(mx, sv[i]);
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -566,7 +579,7 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
                 block(b, r);
             }
         }
-        // The wavefronts' states of this head, merged in wavefront order (as attn_body).
+        // The wavefronts' states of these pairs, merged in wavefront order (as attn_body).
         float L = Lp + __shfl_xor(Lp, 16, 64);
         L += __shfl_xor(L, 32, 64);
         if (g == 0) {
@@ -587,8 +600,8 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
         }
         __syncthreads();
         for (int e = tid; e < ATQ * (HD / 4); e += AWV * 64) {
-            const int tk = e % ATQ, d = 4 * (e / ATQ);
-            if (tk >= nq) continue;
+            const int tk = e % ATQ, d = 4 * (e / ATQ), pr = pt * ATQ + tk;
+            if (pr >= npairs) continue;
             float mw[AWV], Mx = -INFINITY;
 #pragma unroll
             for (int k = 0; k < AWV; k++) {
@@ -605,17 +618,17 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
 #pragma unroll
                 for (int i = 0; i < 4; i++) ow[i] = __builtin_fmaf(x[i], e2, ow[i]);
             }
-            const size_t row = (size_t(i0 + tk) * heads + head) * ASPLIT + s;
+            const size_t row = (size_t(i0 + pr % nq) * heads + grp * hpg + pr / nq) * ASPLIT + s;
             if (d == 0) {
                 st_f32(Mx, rm, int(row * 4));
                 st_f32(Lw, rl, int(row * 4));
             }
             st_attn_f32x4(ow, ro, int((row * HD + d) * 4));
         }
-        __syncthreads();  // before the next head reuses the LDS
+        __syncthreads();  // before the next pair tile reuses the LDS
     }
 
-    // The last workgroup of (group, segment) merges the ASPLIT states of every head in order.
+    // The last workgroup of (group, segment) merges the ASPLIT states of every pair in order.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
@@ -679,10 +692,10 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
         for (int u = 0; u < DPT; u++) Os[pr * HD + sub * DPT + u] = o[u] * inv;
     }
     __syncthreads();
-    uint8_t* tf = frags + size_t(tile) * frag_stride;
     for (int p = tid; p < hpg * nq * (HD / 8); p += AWV * 64) {
         const int pr = p / (HD / 8), sl = p % (HD / 8), hh = pr / nq, i = pr % nq, col = (grp * hpg + hh) * HD + 8 * sl;
-        write_slot(tf, col / 32, tok0 + i + 16 * ((col % 32) / 8), Os + pr * HD + 8 * sl);
+        const int r = i0 + i;  // token r % 16 of tile r / 16 (a segment may straddle two tiles)
+        write_slot(frags + size_t(r / ATQ) * frag_stride, col / 32, r % ATQ + 16 * ((col % 32) / 8), Os + pr * HD + 8 * sl);
     }
 }
 

@@ -1478,12 +1478,13 @@ void Model::verify_greedy_batch(const uint32_t* blocks, const size_t* lens, uint
     }
     for (size_t i = 0; i < rows; i++)
         if (blocks[i] >= cfg_.vocab) fail("token id " + std::to_string(blocks[i]) + " is outside the vocabulary");
-    // Attention segments: each sequence's rows cut at 16-row tile boundaries.
+    // Attention segments: each sequence's rows in pieces of at most 16 from its first row (one
+    // piece for a verify block of up to 16 rows, wherever it sits in the tiles).
     std::vector<int> segs;
     for (int q = 0, r = 0; q < n_seq_; q++) {
         const int end = r + int(lens[q]);
         while (r < end) {
-            const int e = std::min(end, (r / FTOK + 1) * FTOK);
+            const int e = std::min(end, r + int(FTOK));
             segs.insert(segs.end(), {r, e - r, q, 0});
             r = e;
         }
