@@ -1172,19 +1172,21 @@ __device__ __forceinline__ void head_final_last(const MMArgs& a, int* lds) {
 template <int BITS, bool G16>
 constexpr int head_pf() { return BITS == 4 ? (G16 ? 1 : 2) : 3; }
 // Wavefronts per workgroup: 10 give 2560 on 256 CUs, so a 151936-row table (2374 groups of 64)
-// takes at most one group per wavefront; the groups-of-16 variants keep 8 for registers.
-template <bool G16>
-constexpr int head_waves() { return G16 ? 8 : 10; }
-constexpr int HEAD_WAVES_MAX = 10;
+// takes at most one group per wavefront; the groups-of-16 variants keep 8 for registers. A launch
+// over several token tiles (MT) runs 12 (198 workgroups, one group per wavefront): measured on the
+// 0.5B table over 9 tiles, 231 us against 279 us with 10 (one tile: 36-37 us either way).
+template <bool G16, bool MT = false>
+constexpr int head_waves() { return G16 ? 8 : (MT ? 12 : 10); }
+constexpr int HEAD_WAVES_MAX = 12;
 constexpr int HEAD_BMAX = 16;  // fragment slots (16 B) copied to LDS per thread
 constexpr int HEAD_FIN_MAX = 128;  // tokens of a head launch that does its own final reduction
 
 // CMP (one token tile of nt tokens): LDS holds only the live tokens' fragment slots, [k-step][term]
 // [column group][nt], for tables whose full fragments (16 token columns) exceed the LDS; the slots
 // are copied through registers, a few per thread at a time.
-template <int BITS, bool G16, bool CMP = false>
-__global__ __launch_bounds__(64 * head_waves<G16>()) void k_head(MMArgs a, int n_groups) {
-    constexpr int HEAD_WAVES = head_waves<G16>();
+template <int BITS, bool G16, bool CMP = false, bool MT = false>
+__global__ __launch_bounds__((64 * head_waves<G16, MT>())) void k_head(MMArgs a, int n_groups) {
+    constexpr int HEAD_WAVES = head_waves<G16, MT>();
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int Q = Steps<BITS>::Q, HEAD_PF = head_pf<BITS, G16>();
     const TMat& W = a.W;
@@ -1737,7 +1739,8 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
     // One workgroup per CU (the fragments fill most of its LDS).
     const int n_groups = p.nrb;
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
-    const int waves = g16 ? head_waves<true>() : head_waves<false>();
+    const bool mt = p.tiles > 1 && !cmp;
+    const int waves = g16 ? head_waves<true>() : (mt ? head_waves<false, true>() : head_waves<false>());
     const int blocks = std::min(device_cu_count(), (n_groups + waves - 1) / waves);
     const dim3 grid(blocks, p.tiles), block(64 * waves);
     if (cmp) {
@@ -1756,13 +1759,18 @@ int mm_head(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s
         return blocks;
     }
     switch (a.W.bits) {
-        case 16: go(k_head<16, false>, grid, block, lds, s, a, n_groups); break;
+        case 16:
+            if (mt) go(k_head<16, false, false, true>, grid, block, lds, s, a, n_groups);
+            else go(k_head<16, false>, grid, block, lds, s, a, n_groups);
+            break;
         case 8:
             if (g16) go(k_head<8, true>, grid, block, lds, s, a, n_groups);
+            else if (mt) go(k_head<8, false, false, true>, grid, block, lds, s, a, n_groups);
             else go(k_head<8, false>, grid, block, lds, s, a, n_groups);
             break;
         default:
             if (g16) go(k_head<4, true>, grid, block, lds, s, a, n_groups);
+            else if (mt) go(k_head<4, false, false, true>, grid, block, lds, s, a, n_groups);
             else go(k_head<4, false>, grid, block, lds, s, a, n_groups);
             break;
     }
