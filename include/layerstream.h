@@ -218,7 +218,10 @@ int ls_model_debug_fail_next(ls_model* m);
  * flags seen, 14 and 15 stale re-fetch counts, 16 + w wavefront w's products done, 24 the flag's
  * store acknowledged (a timeline makes each unit wait for it). Copies up to cap words of the last
  * pass's stamps to out (NULL: none) and returns the number of words, [workgroup][layer][5
- * stages][32]; 0 when there is no timeline. */
+ * stages][32]; 0 when there is no timeline. Without the persistent pass, LS_STACK_TIMELINE=1 makes
+ * every workgroup of the layer-stack launch record [workgroup][4] stamps: entry, input there (after
+ * its wait; 0 when it has none), done, unused; workgroups in launch order (per layer: q|k|v strips,
+ * attention, o, gate|up, down). */
 size_t ls_model_debug_timeline(ls_model* m, uint64_t* out, size_t cap);
 /* Debugging hook: a copy of one of the model's device buffers by name ("x", "xf", "ss", "q",
  * "af", "actf", "kcache", "vcache", "pass_area"), up to cap bytes (out may be NULL). Returns the

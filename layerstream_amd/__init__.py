@@ -449,17 +449,21 @@ class Model:
         """Replay verify steps from captured HIP graphs (default on; resident weights only)."""
         _check(lib().ls_model_use_graphs(self.h, int(enable)))
 
-    def debug_timeline(self) -> np.ndarray:
+    def debug_timeline(self, raw: bool = False) -> np.ndarray:
         """Per-unit stamps of the last persistent pass (LS_PASS_TIMELINE=1 at creation), or None:
         [workgroup][layer][stage (qkv, attention, o, gate|up, down)][32] in 100 MHz ticks:
         0 start, 1 + w wavefront w's input ready, 9 1/rms known, 10 products summed, 11 stores
         issued, 12 done, 13 flags seen, 14/15 stale re-fetches (counts), 16 + w wavefront w's
-        products done, 24 flag store acknowledged; 0 where a unit did not run or reach a stamp."""
+        products done, 24 flag store acknowledged; 0 where a unit did not run or reach a stamp.
+        With raw, the words as they are: also the layer stack's [workgroup][4] stamps
+        (LS_STACK_TIMELINE=1 at creation: entry, input there, done, unused)."""
         n = lib().ls_model_debug_timeline(self.h, None, 0)
         if n == 0:
             return None
         out = np.zeros(n, np.uint64)
         lib().ls_model_debug_timeline(self.h, out.ctypes.data_as(C.POINTER(C.c_uint64)), n)
+        if raw:
+            return out
         L = self.cfg()["layers"]
         return out.reshape(-1, L, 5, 32)
 

@@ -100,6 +100,7 @@ __device__ __forceinline__ void flow_wait(const Flow& fl, int j, int who) {
                 break;
             __builtin_amdgcn_s_sleep(2);
         }
+        if (fl.stamp) *fl.stamp = __builtin_amdgcn_s_memrealtime();
         if (fl.consumers > 0) {
             const int old = __hip_atomic_fetch_add(c0 + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (old == fl.consumers - 1) {

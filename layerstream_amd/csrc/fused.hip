@@ -254,10 +254,10 @@ void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, fl
 // waiting on fin. With OUT_FLOW the outputs are written through the coherent path and the
 // workgroup then signals fout; for the residual epilogue the residual rows themselves were
 // written in the same launch, so they too are read coherently after the wait.
-template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false, bool PRE = false>
+template <int BITS, int EPI, bool G16, int S, bool IN_FLOW = false, bool OUT_FLOW = false, bool PRE = false, int WD = 1>
 __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const MMScratch& sc, const Flow& fin, const Flow& fout, int bx,
                                         int tile, uint8_t* smem) {
-    constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW;
+    constexpr int Q = Steps<BITS>::Q, CPW = Steps<BITS>::CPW * WD;  // WD: the plan's wide
     const int nw = p.rg * p.kw, nthr = nw * 64;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int rb = bx / p.nsplit, sp = bx % p.nsplit;
@@ -663,12 +663,12 @@ __device__ __forceinline__ void xcd_tile_map(int& bx, int& tile) {
     tile = P % tiles;
 }
 
-template <int BITS, int EPI, bool G16, int S>
-__global__ __launch_bounds__(mm_max_waves(BITS, G16 ? 16 : 32, S) * 64) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
+template <int BITS, int EPI, bool G16, int S, int WD = 1>
+__global__ __launch_bounds__((WD > 1 ? 8 : mm_max_waves(BITS, G16 ? 16 : 32, S)) * 64) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     extern __shared__ __align__(16) uint8_t smem[];
     int bx = blockIdx.x, tile = blockIdx.y;
     if (gridDim.y > 1) xcd_tile_map(bx, tile);
-    mm_body<BITS, EPI, G16, S>(a, p, sc, Flow{}, Flow{}, bx, tile, smem);
+    mm_body<BITS, EPI, G16, S, false, false, false, WD>(a, p, sc, Flow{}, Flow{}, bx, tile, smem);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -963,7 +963,7 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
 // issue their weight loads at once, and only then wait for their input. Counters (per layer,
 // FLOW_LAYER_STRIDE apart): q|k|v -> attention one per head, attention -> o, o -> gate|up,
 // gate|up -> down one per down K split, down -> the next layer's q|k|v.
-template <int HD, int BITS, bool G16>
+template <int HD, int BITS, bool G16, int WD = 1>
 __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
                                                 MMArgs oa, MMPlan po, MMArgs ga, MMPlan pg, MMArgs da, MMPlan pd, MMScratch sc,
                                                 LayerFlows lf) {
@@ -975,6 +975,8 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     const LayerPtrs& P = lp[l];
     const int base = FLOW_COUNTERS + FLOW_LAYER_STRIDE * l;
     const bool last = l + 1 == lf.layers;
+    unsigned long long* tl = lf.tl ? lf.tl + size_t(blockIdx.x) * 4 : nullptr;
+    if (tl && threadIdx.x == 0) tl[0] = __builtin_amdgcn_s_memrealtime();
     if (r < nq) {
         if (int(threadIdx.x) >= 64 * pq.kw) return;
         MMArgs a = qa;
@@ -988,6 +990,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
             fin.producers = fin.per = pd.nrb;
             fin.base = base - FLOW_LAYER_STRIDE + FL_D;
             fin.mirrors = lf.m_d;
+            fin.stamp = tl ? tl + 1 : nullptr;
         }
         Flow fout;
         fout.ctl = lf.ctl;
@@ -1002,7 +1005,8 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
             fout.zero1 = base - FLOW_LAYER_STRIDE + FL_G;
             fout.nzero1 = (pg.nrb + lf.gu_per - 1) / lf.gu_per * lf.m_g;
         }
-        mm_body<BITS, EPI_QKV, G16, 1, true, true, true>(a, pq, sc, fin, fout, r, 0, smem);
+        mm_body<BITS, EPI_QKV, G16, 1, true, true, true, WD>(a, pq, sc, fin, fout, r, 0, smem);
+        if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
     r -= nq;
@@ -1016,12 +1020,14 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fin.producers = nq;
         fin.want = 3 * (HD / 16);
         fin.base = base + FL_Q;
+        fin.stamp = tl ? tl + 1 : nullptr;
         Flow fout;
         fout.ctl = lf.ctl;
         fout.producers = fout.per = aa.heads;
         fout.base = base + FL_A;
         fout.mirrors = lf.m_a;
         attn_body<HD, true, true>(A, r % ASPLIT, r / ASPLIT, 0, fout, smem, fin);
+        if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
     r -= na;
@@ -1050,6 +1056,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fin.producers = fin.per = aa.heads;
         fin.base = base + FL_A;
         fin.mirrors = lf.m_a;
+        fin.stamp = tl ? tl + 1 : nullptr;
         if (r == 0) {
             // Every attention workgroup of this layer, and so every q|k|v workgroup, has finished
             // waiting (all heads merged).
@@ -1060,7 +1067,8 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
                 fo.nzero1 = lf.m_d;
             }
         }
-        mm_body<BITS, EPI_RESID, G16, 1, true, true, true>(a, po, sc, fin, fo, r, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, 1, true, true, true, WD>(a, po, sc, fin, fo, r, 0, smem);
+        if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
     r -= no;
@@ -1073,7 +1081,9 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
             fg.zero0 = base + FL_A;
             fg.nzero0 = lf.m_a;
         }
-        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true, true>(a, pg, sc, fo, fg, r, 0, smem);
+        fo.stamp = tl ? tl + 1 : nullptr;
+        mm_body<BITS, EPI_SILU, G16, gu_wave_strips(BITS, G16 ? 16 : 32), true, true, true, WD>(a, pg, sc, fo, fg, r, 0, smem);
+        if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
     r -= ng;
@@ -1088,7 +1098,9 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.base = base + FL_D;  // back to zero in the next layer's first o workgroup
         fout.mirrors = lf.m_d;
     }
-    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true>(a, pd, sc, fg, fout, r, 0, smem);
+    fg.stamp = tl ? tl + 1 : nullptr;
+    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true, WD>(a, pd, sc, fg, fout, r, 0, smem);
+    if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
 }
 
 // The head's last workgroup to finish: partials were stored at agent scope and waited on before
@@ -1356,14 +1368,18 @@ int device_cu_count() {
 
 constexpr size_t HEAD_LDS_MAX = 150 * 1024;
 
-MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips, int wide) {
     MMPlan p;
     if (strips != 1 && strips != 2 && strips != 4) throw std::runtime_error("1, 2 or 4 strips per wavefront");
+    if (wide != 1 && wide != 2) throw std::runtime_error("a wavefront's share of K is 128 or 256 columns");
+    if (wide == 2 && W.bits != 16 && W.group == 16) throw std::runtime_error("256-column shares need groups of 32 or more");
     p.s = strips;
     p.rg = rg;
     p.kw = kw < 1 ? 1 : kw;
-    const int max_waves = mm_max_waves(W.bits, W.group, strips);
-    const int cpw = 4 / (W.bits == 16 ? 1 : (W.bits == 8 ? 2 : 4));
+    p.wide = wide;
+    // 256-column shares double the registers that hold weights and fragments: 8 wavefronts at most.
+    const int max_waves = wide > 1 ? 8 : mm_max_waves(W.bits, W.group, strips);
+    const int cpw = wide * 4 / (W.bits == 16 ? 1 : (W.bits == 8 ? 2 : 4));
     const int waves_k = (W.n_chunks + cpw - 1) / cpw;  // wavefront shares along K
     if (p.kw > waves_k) p.kw = waves_k;
     if (p.rg > max_waves) throw std::runtime_error("too many row groups for one workgroup");
@@ -1381,9 +1397,9 @@ MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips) {
     return p;
 }
 
-MMPlan gu_plan(const TMat& W, int kw, int n_tokens) {
+MMPlan gu_plan(const TMat& W, int kw, int n_tokens, int wide) {
     const int gs = gu_wave_strips(W.bits, W.group);
-    return mm_plan(W, 2 * GU_STRIPS / gs, kw, n_tokens, gs);
+    return mm_plan(W, 2 * GU_STRIPS / gs, kw, n_tokens, gs, wide);
 }
 
 size_t mm_part_floats(const MMPlan& p) {
@@ -1424,6 +1440,16 @@ static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStr
     const dim3 grid(p.nrb * p.nsplit, p.tiles), block(64 * p.rg * p.kw);
     const size_t lds = lds_bytes(p, EPI == EPI_QKV ? a.hd : 0);
     const bool g16 = a.W.bits != 16 && a.W.group == 16;
+    if (p.wide != 1) {
+        if (p.wide != 2 || g16) throw std::runtime_error("256-column shares need groups of 32 or more");
+        switch (a.W.bits) {
+            case 16: go(k_mm<16, EPI, false, S, 2>, grid, block, lds, s, a, p, sc); break;
+            case 8: go(k_mm<8, EPI, false, S, 2>, grid, block, lds, s, a, p, sc); break;
+            default: go(k_mm<4, EPI, false, S, 2>, grid, block, lds, s, a, p, sc); break;
+        }
+        FCHECK(hipGetLastError());
+        return;
+    }
     switch (a.W.bits) {
         case 16: go(k_mm<16, EPI, false, S>, grid, block, lds, s, a, p, sc); break;
         case 8:
@@ -1473,7 +1499,7 @@ bool mm_gate_up_pipe_fits(const MMArgs& a, const MMPlan& p) {
     int gk = 0;
     // 8 wavefronts of 2 shares each, one tile, no K split; byte offsets (past-the-end items
     // included) below 2^31.
-    if (p.tiles != 1 || p.rg != 1 || p.kw != PIPE_WAVES * PIPE_SPW || p.nsplit != 1 || p.s != 2 * GU_STRIPS) return false;
+    if (p.wide != 1 || p.tiles != 1 || p.rg != 1 || p.kw != PIPE_WAVES * PIPE_SPW || p.nsplit != 1 || p.s != 2 * GU_STRIPS) return false;
     if (!pipe_group_steps(a.W, gk)) return false;
     return tile_data_bytes(a.W) <= PIPE_MAX_BYTES && tile_scale_bytes(a.W) <= PIPE_MAX_BYTES;
 }
@@ -1507,6 +1533,7 @@ void mm_gate_up_down(const MMArgs& gu, const MMPlan& pgu, const MMArgs& dn, cons
         throw std::runtime_error("gate|up/down plans do not match");
     if (pgu.tiles != 1 || pdn.tiles != 1) throw std::runtime_error("the fused gate|up/down launch takes one token tile");
     if (pgu.nsplit != 1) throw std::runtime_error("the fused gate|up/down launch needs gate|up without a K split");
+    if (pgu.wide != 1 || pdn.wide != 1) throw std::runtime_error("the fused gate|up/down launch takes 128-column K shares");
     if (pdn.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
     // A down K split covers 128 kw columns (4 k-steps of 32 per wavefront); a gate|up row block
     // produces 16 GU_STRIPS of them.
@@ -1563,6 +1590,7 @@ void attention_o(const float* q, int ldq, int t, int heads, int kv_heads, int hd
                  hipStream_t s) {
     if (t > FTOK || po.tiles != 1) throw std::runtime_error("the fused attention/o launch takes one token tile");
     if (po.s != 1 || po.nsplit != 1) throw std::runtime_error("the fused attention/o launch needs o without a K split");
+    if (po.wide != 1) throw std::runtime_error("the fused attention/o launch takes 128-column K shares");
     if (64 * po.rg * po.kw > 512) throw std::runtime_error("o workgroups too large for the fused attention/o launch");
     const AttnArgs aa = make_attn_args(q, ldq, t, heads, kv_heads, hd, pos0, AttnRows{}, kc, vc, scratch, cnt, frags);
     Flow fl;
@@ -1611,6 +1639,7 @@ void qkv_attention_o(const MMArgs& qa, const MMPlan& pq, float* scratch, int* cn
     if (t < 1 || t > FTOK || pq.tiles != 1 || po.tiles != 1) throw std::runtime_error("the fused q|k|v/attention/o launch takes one token tile");
     if (pq.s != 1 || pq.rg != 1 || pq.nsplit != 1) throw std::runtime_error("the fused launch needs q|k|v as one workgroup per strip");
     if (po.s != 1 || po.nsplit != 1) throw std::runtime_error("the fused launch needs o without a K split");
+    if (pq.wide != 1 || po.wide != 1) throw std::runtime_error("the fused launch takes 128-column K shares");
     if (64 * po.rg * po.kw > 512 || 64 * pq.kw > 512) throw std::runtime_error("workgroups too large for the fused launch");
     if (heads > FLOW_ATTN_O || hd % 16 || heads % kvh) throw std::runtime_error("heads do not fit the fused launch's counters");
     if (hd / 2 > ROPE_HALF_MAX || (heads + kvh) * hd % 16) throw std::runtime_error("head_dim must be even and at most 256");
@@ -1651,7 +1680,9 @@ const char* layer_stack_unfit(int t, int heads, int kv_heads, int hd, const MMPl
     if (pg.nsplit != 1 || pg.s * pg.rg != 2 * GU_STRIPS) return "the layer stack needs gate|up row blocks without a K split";
     if (pd.s != DOWN_STRIPS) return "the layer stack needs the down plan's strips per wavefront";
     if (pd.nsplit * FLOW_GU_MIRRORS > FLOW_LAYER_STRIDE - FL_G) return "too many down K splits for the layer counters";
-    const int split_cols = 128 * pd.kw, act_cols = 16 * GU_STRIPS;
+    if (pq.wide != pd.wide || po.wide != pd.wide || pg.wide != pd.wide) return "the layer's plans differ in their K shares";
+    if (pd.wide != 1 && hd != 128) return "256-column K shares run in the layer stack for head_dim 128 only";
+    const int split_cols = 128 * pd.wide * pd.kw, act_cols = 16 * GU_STRIPS;
     if (split_cols % act_cols || (pg.nrb + split_cols / act_cols - 1) / (split_cols / act_cols) != pd.nsplit)
         return "gate|up row blocks do not map onto the down K splits";
     if (std::max({64 * pq.kw, AWV * 64, 64 * po.rg * po.kw, 64 * pg.rg * pg.kw, 64 * pd.rg * pd.kw}) > 512)
@@ -1674,6 +1705,19 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
     const size_t lds = std::max({lds_bytes(pq, qa.hd), lds_bytes(po), lds_bytes(pg), lds_bytes(pd), attn_lds_bytes<HD>(),
                                  size_t(96) << 10});
     const bool g16 = qa.W.bits != 16 && qa.W.group == 16;
+    if constexpr (HD == 128) {
+        if (pq.wide == 2) {
+            if (g16) throw std::runtime_error("256-column shares need groups of 32 or more");
+            switch (qa.W.bits) {
+                case 16: go(k_layers<HD, 16, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+                case 8: go(k_layers<HD, 8, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+                default: go(k_layers<HD, 4, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+            }
+            FCHECK(hipGetLastError());
+            return;
+        }
+    }
+    if (pq.wide != 1) throw std::runtime_error("256-column K shares run in the layer stack for head_dim 128 only");
     switch (qa.W.bits) {
         case 16: go(k_layers<HD, 16, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
         case 8:
@@ -1690,7 +1734,7 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
 
 void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& qa, const MMPlan& pq, float* attn_scratch, int* attn_cnt,
                  uint8_t* af, const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da,
-                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s) {
+                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s, unsigned long long* timeline) {
     const int heads = qa.heads, kvh = qa.kv_heads, hd = qa.hd, t = qa.n;
     if (const char* why = layer_stack_unfit(t, heads, kvh, hd, pq, po, pg, pd)) throw std::runtime_error(why);
     if (pd.nsplit > 1 && (!sc.part || !sc.cnt)) throw std::runtime_error("split matrix launch without scratch");
@@ -1699,7 +1743,8 @@ void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& 
     LayerFlows lf;
     lf.ctl = ctl;
     lf.layers = layers;
-    lf.gu_per = 128 * pd.kw / (16 * GU_STRIPS);
+    lf.tl = timeline;
+    lf.gu_per = 128 * pd.wide * pd.kw / (16 * GU_STRIPS);
     lf.m_a = std::min<int>(FL_MIRRORS, po.nrb);
     lf.m_o = std::min<int>(FL_MIRRORS, pg.nrb);
     lf.m_d = std::min<int>(FL_MIRRORS, pq.nrb);

@@ -141,9 +141,12 @@ struct MMArgs {
 // Work split of one launch: each wavefront streams s strips (16 s rows); a workgroup owns rg
 // such row groups and one of nsplit K ranges, cut among kw wavefronts per row group. With
 // nsplit > 1 the pieces meet in `part` and the last workgroup of a row block to finish adds them
-// in split order (counters in `cnt` start at zero and are left at zero).
+// in split order (counters in `cnt` start at zero and are left at zero). A wavefront's share of K
+// is 128 columns, or 256 when wide is 2 (hidden sizes of 2048 and more: 8 wavefronts then cover
+// the row without a split, so every role of such a layer fits a 512-thread workgroup). The share
+// decides the summation order, so every launch of a model uses the same wide.
 struct MMPlan {
-    int s = 1, rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1;
+    int s = 1, rg = 1, kw = 1, nsplit = 1, nrb = 1, tiles = 1, wide = 1;
 };
 // Wavefronts a matrix workgroup may hold: 16 (1024 threads, at most 128 registers each), but 8
 // for four bf16 or groups-of-16 strips per wavefront, whose wider chunks or extra MFMAs need more
@@ -151,9 +154,9 @@ struct MMPlan {
 __host__ __device__ constexpr int mm_max_waves(int bits, int group, int strips) {
     return (strips == 4 && (bits == 16 || group == 16)) ? 8 : 16;
 }
-MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips);
+MMPlan mm_plan(const TMat& W, int rg, int kw, int n_tokens, int strips, int wide = 1);
 // The gate|up plan: gu_wave_strips strips per wavefront, row groups making one gate and up block.
-MMPlan gu_plan(const TMat& W, int kw, int n_tokens);
+MMPlan gu_plan(const TMat& W, int kw, int n_tokens, int wide = 1);
 size_t mm_part_floats(const MMPlan& p);
 size_t mm_counters(const MMPlan& p);
 
@@ -192,6 +195,8 @@ struct Flow {
     // first, count), for flows whose consumers (consumers == 0: they do not count themselves)
     // have all finished waiting by then.
     int zero0 = 0, nzero0 = 0, zero1 = 0, nzero1 = 0;
+    // When set, the wait stores the s_memrealtime count (100 MHz) at which its input was there.
+    unsigned long long* stamp = nullptr;
 };
 // Control block words: error flag, greedy acceptance (m, next), the head's finished-workgroup
 // count (its own 128-byte line), then the counter slots (gate|up
@@ -265,6 +270,9 @@ struct LayerFlows {
     int layers = 0;
     int gu_per = 1;                      // gate|up row blocks per down K split
     int m_a = 1, m_o = 1, m_d = 1, m_g = 1;  // copies of the attention -> o, o -> gate|up, down -> q|k|v, gate|up -> down counters
+    // Per-workgroup timeline (LS_STACK_TIMELINE=1), [workgroup][4] s_memrealtime counts: entry,
+    // input there (after the wait), done; word 3 is unused.
+    unsigned long long* tl = nullptr;
 };
 // Workgroups of one layer in the layer-stack launch.
 int layer_stack_workgroups(int heads, const MMPlan& pq, const MMPlan& po, const MMPlan& pg, const MMPlan& pd);
@@ -278,7 +286,7 @@ const char* layer_stack_unfit(int t, int heads, int kv_heads, int hd, const MMPl
 // the last layer are left for the head. ctl holds flow_words(layers) words, zero between launches.
 void layer_stack(const LayerPtrs* lp, int layers, size_t seq_off, const MMArgs& qa, const MMPlan& pq, float* attn_scratch, int* attn_cnt,
                  uint8_t* af, const MMArgs& oa, const MMPlan& po, const MMArgs& ga, const MMPlan& pg, const MMArgs& da,
-                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s);
+                 const MMPlan& pd, const MMScratch& sc, int* ctl, hipStream_t s, unsigned long long* timeline = nullptr);
 
 // Output head (plan strips 4, rg 1): logits (1/rms applied), optional logits store, argmax
 // partials at [tile][arg_off + b][16] for b below the returned count. With a.fin_cnt (one head

@@ -691,8 +691,17 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const size_t n_chunks = (c.vocab + STREAM_HEAD_ROWS - 1) / STREAM_HEAD_ROWS;
         head_blocks_ = std::max(e_res.n_strips / 4, int(n_chunks * STREAM_HEAD_ROWS / 64));
     }
-    // Wide rows (3B: 32 int8 chunks) fill a 16-wavefront workgroup along K with no split.
-    if (c.hidden >= 2048) kw_qkv_ = kw_o_ = kw_gu_ = kw_down_ = kw_head_ = 16;
+    // Wide rows (3B: 32 int8 chunks): 256-column K shares, so 8 wavefronts cover a row of 2048
+    // with no split and every role of a layer fits the layer stack's 512-thread workgroups
+    // (LS_WIDE=0: 128-column shares, 16 wavefronts; not for weights in groups of 16). The head has
+    // its own plan.
+    const bool g16w = c.format.bits != 16 && c.format.group == 16;
+    if (c.hidden >= 2048) {
+        wide_ = g16w ? 1 : 2;
+        if (const char* e = std::getenv("LS_WIDE"); e && std::atoi(e) == 0) wide_ = 1;
+        kw_qkv_ = kw_o_ = kw_gu_ = kw_down_ = wide_ == 2 ? 8 : 16;
+        kw_head_ = 16;
+    }
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
     if (const char* e = std::getenv("LS_FUSE_QKV")) fuse_qkv_ = std::atoi(e) != 0;
@@ -718,8 +727,8 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const int n = int(T);
         const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(STREAM_HEAD_ROWS), int(h), 256);
-        const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1),        mm_plan(la.o, 1, kw_o_, n, 1),
-                                gu_plan(la.gu, kw_gu_, n), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS),
+        const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1, wide_),  mm_plan(la.o, 1, kw_o_, n, 1, wide_),
+                                gu_plan(la.gu, kw_gu_, n, wide_), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS, wide_),
                                 mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};
         size_t pf = 0, nc = 0;
         for (const MMPlan& pl : plans) {
@@ -771,8 +780,13 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         // The persistent pass, when its plans fit (the plans of a one-tile pass do not depend on
         // its token count).
         const DevLayer& L0 = prov_->layer(0);
-        const MMPlan pq = mm_plan(L0.qkv, 1, kw_qkv_, 1, 1), po = mm_plan(L0.o, 1, kw_o_, 1, 1);
-        const MMPlan pg = gu_plan(L0.gu, kw_gu_, 1), pd = mm_plan(L0.down, 1, kw_down_, 1, DOWN_STRIPS);
+        const MMPlan pq = mm_plan(L0.qkv, 1, kw_qkv_, 1, 1, wide_), po = mm_plan(L0.o, 1, kw_o_, 1, 1, wide_);
+        const MMPlan pg = gu_plan(L0.gu, kw_gu_, 1, wide_), pd = mm_plan(L0.down, 1, kw_down_, 1, DOWN_STRIPS, wide_);
+        if (const char* e = std::getenv("LS_STACK_TIMELINE"); e && std::atoi(e) != 0 && !layer_stack_unfit(1, int(c.heads), int(c.kv_heads), int(c.head_dim), pq, po, pg, pd)) {
+            // Per-workgroup stamps of the layer stack (entry, input there, done), for profiling.
+            stack_tl_ = DevBuf(size_t(c.layers) * layer_stack_workgroups(int(c.heads), pq, po, pg, pd) * 4 * 8);
+            HIPC(hipMemsetAsync(stack_tl_.p, 0, stack_tl_.n, stream_));
+        }
         if (const char* e = std::getenv("LS_PASS")) pass_on_ = std::atoi(e) != 0;  // persistent pass (default off)
         if (pass_on_ && !layer_pass_unfit(1, int(c.heads), int(c.kv_heads), int(c.head_dim), pq, po, pg, pd) && c.layers < 64) {
             int repl = 1;  // copies of the exchange buffers that many units read at once (LS_PASS_COPIES)
@@ -940,8 +954,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
         // One launch for every layer: the same plans (so the same bits) as the per-layer
         // launches below.
-        const MMPlan pq = mm_plan(L0->qkv, 1, kw_qkv_, T, 1), po = mm_plan(L0->o, 1, kw_o_, T, 1);
-        const MMPlan pg = gu_plan(L0->gu, kw_gu_, T), pd = mm_plan(L0->down, 1, kw_down_, T, DOWN_STRIPS);
+        const MMPlan pq = mm_plan(L0->qkv, 1, kw_qkv_, T, 1, wide_), po = mm_plan(L0->o, 1, kw_o_, T, 1, wide_);
+        const MMPlan pg = gu_plan(L0->gu, kw_gu_, T, wide_), pd = mm_plan(L0->down, 1, kw_down_, T, DOWN_STRIPS, wide_);
         if (!layer_stack_unfit(T, heads, kvh, hd, pq, po, pg, pd)) {
             MMArgs qa;
             qa.W = L0->qkv;
@@ -998,7 +1012,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                            ctl_.as<int>(), epoch_.as<int>(), pass_tl_.p ? pass_tl_.as<uint64_t>() : nullptr, s);
             } else {
                 layer_stack(layer_ptrs_.as<LayerPtrs>(), int(c.layers), size_t(cur_) * max_ctx_ * kv, qa, pq, attn_scratch_.as<float>(),
-                            attn_cnt_.as<int>(), af_.as<uint8_t>(), oa, po, ga, pg, da, pd, scr, ctl_.as<int>(), s);
+                            attn_cnt_.as<int>(), af_.as<uint8_t>(), oa, po, ga, pg, da, pd, scr, ctl_.as<int>(), s,
+                            stack_tl_.p ? stack_tl_.as<unsigned long long>() : nullptr);
             }
             for (size_t l = 0; l < c.layers; l++) {
                 const DevLayer& L = prov_->layer(l);
@@ -1047,7 +1062,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.kv_heads = kvh;
             a.hd = hd;
         }
-        const MMPlan pq = mm_plan(L.qkv, 1, kw_qkv_, T, 1);
+        const MMPlan pq = mm_plan(L.qkv, 1, kw_qkv_, T, 1, wide_);
         {
             MMArgs a;
             a.W = L.o;
@@ -1061,14 +1076,14 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.onorm = L.post_norm;
             a.oss = ss;
             a.oss_slots = slots_h_;
-            const MMPlan po = mm_plan(L.o, 1, kw_o_, T, 1);
+            const MMPlan po = mm_plan(L.o, 1, kw_o_, T, 1, wide_);
             // One launch for attention and o when the o workgroups can fetch their weights while
             // attention runs (one token tile, every workgroup resident at once); q|k|v joins it
             // when it runs as one workgroup per strip, and attention then fetches the cached
             // keys and values while q|k|v runs.
-            const bool fuse_ao = fuse_on_ && !bv && po.tiles == 1 && po.nsplit == 1 && 64 * po.rg * po.kw <= 512 &&
+            const bool fuse_ao = fuse_on_ && !bv && po.tiles == 1 && po.nsplit == 1 && po.wide == 1 && 64 * po.rg * po.kw <= 512 &&
                                  attention_o_workgroups(heads, po) <= device_cu_count();
-            const bool fuse_qao = fuse_ao && fuse_qkv_ && pq.s == 1 && pq.rg == 1 && pq.nsplit == 1 && 64 * pq.kw <= 512 &&
+            const bool fuse_qao = fuse_ao && fuse_qkv_ && pq.s == 1 && pq.rg == 1 && pq.nsplit == 1 && pq.wide == 1 && 64 * pq.kw <= 512 &&
                                   heads <= FLOW_ATTN_O && qkv_attention_o_workgroups(heads, pq, po) <= device_cu_count();
             if (pf_on_) {
                 // While waiting for attention, the o workgroups read this layer's gate|up and
@@ -1137,12 +1152,12 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 d.pf = N.qkv.data;
                 d.pf_bytes = size_t(end - N.qkv.data);
             }
-            const MMPlan pg = gu_plan(L.gu, kw_gu_, T), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS);
+            const MMPlan pg = gu_plan(L.gu, kw_gu_, T, wide_), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS, wide_);
             // Fused only when both roles fit on the device at one workgroup per CU (their
             // wavefronts fill a CU's register file): a down workgroup that started after a
             // gate|up one had finished would fetch its weights late. Either path gives the same
             // bits (same plans).
-            if (fuse_on_ && pg.tiles == 1 && pg.nsplit == 1 && pg.nrb + pd.nrb * pd.nsplit <= device_cu_count()) {
+            if (fuse_on_ && pg.tiles == 1 && pg.nsplit == 1 && pg.wide == 1 && pg.nrb + pd.nrb * pd.nsplit <= device_cu_count()) {
                 // One launch: the down workgroups fetch their weights while gate|up runs.
                 prof_begin();
                 mm_gate_up_down(g, pg, d, pd, scr, ctl_.as<int>(), s);
@@ -1285,10 +1300,11 @@ void Model::verify_body(const uint32_t* block, size_t n) {
 }
 
 size_t Model::debug_timeline(uint64_t* out, size_t cap) {
-    if (!pass_tl_.p) return 0;
+    const DevBuf& t = pass_tl_.p ? pass_tl_ : stack_tl_;
+    if (!t.p) return 0;
     HIPC(hipStreamSynchronize(stream_));
-    const size_t words = pass_tl_.n / 8;
-    if (out && cap) HIPC(hipMemcpy(out, pass_tl_.p, std::min(cap, words) * 8, hipMemcpyDeviceToHost));
+    const size_t words = t.n / 8;
+    if (out && cap) HIPC(hipMemcpy(out, t.p, std::min(cap, words) * 8, hipMemcpyDeviceToHost));
     return words;
 }
 

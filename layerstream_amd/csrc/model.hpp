@@ -195,6 +195,7 @@ private:
     DevBuf x_, q_, xf_, ss_, af_, actf_, part_, cnt_, attn_scratch_, attn_cnt_, logits_, hpv_, hpi_, row0_, amax_, ctl_, bacc_;
     // Resident models: every layer's pointers for the layer-stack launch (LayerPtrs per layer).
     DevBuf layer_ptrs_;
+    DevBuf stack_tl_;  // layer-stack timeline (LS_STACK_TIMELINE=1): [workgroup][4] stamps
     // The persistent pass (one-tile passes over resident layers; LS_PASS=0: the layer stack): its
     // exchange area, flag lines and epoch word (bumped by the embedding kernel before each pass),
     // and per-unit timeline stamps when LS_PASS_TIMELINE=1.
@@ -215,6 +216,7 @@ private:
     size_t head_off_ = 0;  // launch row of the first requested head row
     // wavefronts along K per row group: q|k|v, o, gate|up, down, head
     int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 8, kw_head_ = 7;
+    int wide_ = 1;  // K share of a wavefront in 128-column units (MMPlan::wide) for every layer matrix
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     int prof_ = 0;  // profiling mode (set_profiling)

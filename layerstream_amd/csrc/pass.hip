@@ -1119,6 +1119,7 @@ size_t pass_timeline_words(int layers) { return size_t(device_cu_count()) * laye
 const char* layer_pass_unfit(int t, int heads, int kv_heads, int hd, const MMPlan& pq, const MMPlan& po, const MMPlan& pg,
                              const MMPlan& pd) {
     if (t > FTOK) return "the persistent pass takes one token tile";
+    if (pq.wide != 1 || po.wide != 1 || pg.wide != 1 || pd.wide != 1) return "the persistent pass takes 128-column K shares";
     if (hd != 16 && hd != 32 && hd != 64) return "head_dim must be 16, 32 or 64";
     if ((heads * hd) % 32 || hd % 16) return "q|k|v rows must fill whole k-steps";
     if (heads % kv_heads) return "heads must be a multiple of kv_heads";

@@ -406,6 +406,8 @@ def test_qwen05b_int8_greedy_after_a_512_token_prompt_matches_the_oracle():
 def qwen3b(fmt, seed=1):
     text = LS.qwen2_config_text(**LS.QWEN2_3B)
     m = LS.synth_bf16_model(text, seed)
+    if fmt is None:
+        return m
     img = LS.quantize_model(text, m["layers"], m["embed"], m["norm"], fmt)
     del m
     parts = T.split_lsq(img.tobytes(), oracle_cfg(LS.inject_quant(text, *fmt)))
@@ -519,21 +521,22 @@ def test_qwen3b_int8_verify_step_matches_the_oracle():
     verify_step_vs_oracle(m, prompt, 8, rng, 256, "3B int8:")
 
 
-def test_qwen3b_pipelined_matrices_give_the_bits_of_k_mm():
-    """Over one token tile the 3B gate|up (688 gate and up strip pairs) has more strip pairs than
-    the device has CUs and runs as the pipelined launch; LS_PIPE=0 runs it as k_mm. Same plan, so
-    the same logits bit for bit and the same acceptance, over blocks of 9, 1 and 9 tokens in a row
-    (the first 40-token prompt runs k_mm over three tiles either way)."""
-    say("3B pipelined vs k_mm: build")
-    m = qwen3b((8, 64))
+def _same_bits_two_ways(m, env_a, env_b, what):
+    """Two models of m, each created under its own engine switches, give the same logits bit for
+    bit and the same acceptance over a 40-token prompt (three tiles) and blocks of 9, 1 and 9
+    tokens in a row."""
     rng = np.random.default_rng(5)
     prompt = rng.integers(0, 151936, 40).tolist()
-    with env("LS_PIPE", "0"):
-        a = gpu_model(m, max_ctx=256)
-    b = gpu_model(m, max_ctx=256)
+    made = []
+    for sw in (env_a, env_b):
+        with contextlib.ExitStack() as st:
+            for k, v in sw.items():
+                st.enter_context(env(k, v))
+            made.append(gpu_model(m, max_ctx=256))
+    a, b = made
     assert np.array_equal(bits(a.forward(prompt)), bits(b.forward(prompt)))
     for block in ([8, 9, 400, 33, 120, 5, 77, 301, 2], [17], [3, 4, 5, 6, 7, 8, 9, 10, 11]):
-        say("3B pipelined vs k_mm: block of", len(block))
+        say(what, "block of", len(block))
         p = a.pos()
         va, vb = a.forward_multi(block, len(block)), b.forward_multi(block, len(block))
         assert np.array_equal(bits(va), bits(vb)), len(block)
@@ -541,6 +544,23 @@ def test_qwen3b_pipelined_matrices_give_the_bits_of_k_mm():
         b.truncate(p)
         assert a.verify_greedy(block) == b.verify_greedy(block), len(block)
         assert a.pos() == b.pos()
+
+
+def test_qwen3b_pipelined_matrices_give_the_bits_of_k_mm():
+    """With 128-column K shares (LS_WIDE=0: 16 wavefronts along a 2048 row) the 3B gate|up over
+    one token tile (688 gate and up strip pairs, more than the device has CUs) runs as the
+    pipelined launch; LS_PIPE=0 runs it as k_mm. Same plan, so the same bits."""
+    say("3B pipelined vs k_mm: build")
+    _same_bits_two_ways(qwen3b((8, 64)), {"LS_WIDE": "0", "LS_PIPE": "0"}, {"LS_WIDE": "0"}, "3B pipelined vs k_mm:")
+
+
+def test_qwen3b_layer_stack_and_per_layer_launches_give_identical_bits():
+    """The 3B shape's default plans use 256-column K shares (8 wavefronts cover a 2048 row), so its
+    one-tile passes run as the layer stack (k_layers, head_dim 128, 256-column shares); LS_STACK=0
+    runs the per-layer k_mm launches with the same plans. Same bits, int8-g64, int4-g32 and bf16."""
+    for fmt in ((8, 64), (4, 32), None):
+        say("3B stack vs per-layer: build", fmt)
+        _same_bits_two_ways(qwen3b(fmt), {"LS_STACK": "0"}, {}, f"3B stack vs per-layer {fmt}:")
 
 
 def test_qwen05b_int4_verify_step_after_a_long_prompt_matches_the_oracle():
