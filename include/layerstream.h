@@ -219,9 +219,10 @@ int ls_model_debug_fail_next(ls_model* m);
  * store acknowledged (a timeline makes each unit wait for it). Copies up to cap words of the last
  * pass's stamps to out (NULL: none) and returns the number of words, [workgroup][layer][5
  * stages][32]; 0 when there is no timeline. Without the persistent pass, LS_STACK_TIMELINE=1 makes
- * every workgroup of the layer-stack launch record [workgroup][4] stamps: entry, input there (after
- * its wait; 0 when it has none), done, unused; workgroups in launch order (per layer: q|k|v strips,
- * attention, o, gate|up, down). */
+ * every workgroup of the layer-stack launch record [workgroup][8] stamps: 0 entry, 1 input there
+ * (after its wait; 0 when it has none), 2 done, and for the matrix roles 3 inputs loaded, 4 products
+ * issued, 5 row-group sums done, 6 epilogue stores issued (7 unused); workgroups in launch order
+ * (per layer: q|k|v, attention, o, gate|up, down). */
 size_t ls_model_debug_timeline(ls_model* m, uint64_t* out, size_t cap);
 /* Debugging hook: a copy of one of the model's device buffers by name ("x", "xf", "ss", "q",
  * "af", "actf", "kcache", "vcache", "pass_area"), up to cap bytes (out may be NULL). Returns the

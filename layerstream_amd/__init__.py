@@ -456,7 +456,8 @@ class Model:
         issued, 12 done, 13 flags seen, 14/15 stale re-fetches (counts), 16 + w wavefront w's
         products done, 24 flag store acknowledged; 0 where a unit did not run or reach a stamp.
         With raw, the words as they are: also the layer stack's [workgroup][4] stamps
-        (LS_STACK_TIMELINE=1 at creation: entry, input there, done, unused)."""
+        (LS_STACK_TIMELINE=1 at creation: [workgroup][8]: entry, input there, done, inputs loaded,
+        products issued, row-group sums done, epilogue stores issued, unused)."""
         n = lib().ls_model_debug_timeline(self.h, None, 0)
         if n == 0:
             return None

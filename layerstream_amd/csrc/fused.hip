@@ -394,12 +394,17 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         }
     }
 
+    if (a.tlw && threadIdx.x == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        a.tlw[3] = __builtin_amdgcn_s_memrealtime();
+    }
     f32x4 total[S], acc[S];
 #pragma unroll
     for (int r = 0; r < S; r++) total[r] = acc[r] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < CPW; c++)
         if (c < nch) chunk_mfma<BITS, G16, S, PRE>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total, scl[PRE ? c : 0]);
+    if (a.tlw && threadIdx.x == 0) a.tlw[4] = __builtin_amdgcn_s_memrealtime();
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
     // rows 16 r + 4 (l / 16) + i of token l % 16. Wavefront 0 works out 1 / rms (read after the
     // barriers below) while the other wavefronts finish their products.
@@ -433,6 +438,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             for (int i = 0; i < 4; i++) tl[(16 * (S * rgi + r) + 4 * (lane >> 4) + i) * FTOK + (lane & 15)] = total[r][i];
     }
     __syncthreads();
+    if (a.tlw && threadIdx.x == 0) a.tlw[5] = __builtin_amdgcn_s_memrealtime();
 
     // Split K: store this piece; the last workgroup of the row block adds all pieces in split
     // order. Pieces move with 128-bit sc1 buffer accesses and the counter with an agent-scope
@@ -510,7 +516,8 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
             }
         }
-        if constexpr (OUT_FLOW) qkv_signal(fout, rb, a.heads, a.kv_heads, a.hd);
+        if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
+        if constexpr (OUT_FLOW) qkv_signal(fout, rb * S, a.heads, a.kv_heads, a.hd);
     } else if constexpr (EPI == EPI_RESID) {
         if constexpr (XCOH) {
             // Residual rows, fragments and partials all go through the coherent path. The new
@@ -571,6 +578,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 if (e < rows_wg * FTOK && tok < nt && row < W.rows)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xr[u]), rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1);
             }
+            if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
             flow_signal(fout, rb);
         }
     } else if constexpr (EPI == EPI_SILU) {
@@ -601,6 +609,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             if constexpr (OUT_FLOW) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
             else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
+        if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
         if constexpr (OUT_FLOW) flow_signal(fout, rb);
     } else {
         // Output head: logits, optional store, per-token best (value, index) of this block.
@@ -963,7 +972,8 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
 // issue their weight loads at once, and only then wait for their input. Counters (per layer,
 // FLOW_LAYER_STRIDE apart): q|k|v -> attention one per head, attention -> o, o -> gate|up,
 // gate|up -> down one per down K split, down -> the next layer's q|k|v.
-template <int HD, int BITS, bool G16, int WD = 1>
+// QS, OS, DS: strips per wavefront of q|k|v, o and down (WD and the strips: the plans' wide and s).
+template <int HD, int BITS, bool G16, int WD = 1, int QS = 1, int OS = 1, int DS = DOWN_STRIPS>
 __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
                                                 MMArgs oa, MMPlan po, MMArgs ga, MMPlan pg, MMArgs da, MMPlan pd, MMScratch sc,
                                                 LayerFlows lf) {
@@ -975,12 +985,13 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     const LayerPtrs& P = lp[l];
     const int base = FLOW_COUNTERS + FLOW_LAYER_STRIDE * l;
     const bool last = l + 1 == lf.layers;
-    unsigned long long* tl = lf.tl ? lf.tl + size_t(blockIdx.x) * 4 : nullptr;
+    unsigned long long* tl = lf.tl ? lf.tl + size_t(blockIdx.x) * 8 : nullptr;
     if (tl && threadIdx.x == 0) tl[0] = __builtin_amdgcn_s_memrealtime();
     if (r < nq) {
         if (int(threadIdx.x) >= 64 * pq.kw) return;
         MMArgs a = qa;
         a.W = P.qkv;
+        a.tlw = tl;
         a.bias = P.b_qkv;
         a.kcache = P.kc + seq_off;
         a.vcache = P.vc + seq_off;
@@ -995,7 +1006,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         Flow fout;
         fout.ctl = lf.ctl;
         fout.producers = nq;
-        fout.want = 3 * (HD / 16);
+        fout.want = 3 * (HD / 16) / QS;
         fout.base = base + FL_Q;
         if (l > 0 && r == 0) {
             // Every workgroup of the previous layer's gate|up and down has finished waiting (the
@@ -1005,7 +1016,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
             fout.zero1 = base - FLOW_LAYER_STRIDE + FL_G;
             fout.nzero1 = (pg.nrb + lf.gu_per - 1) / lf.gu_per * lf.m_g;
         }
-        mm_body<BITS, EPI_QKV, G16, 1, true, true, true, WD>(a, pq, sc, fin, fout, r, 0, smem);
+        mm_body<BITS, EPI_QKV, G16, QS, true, true, true, WD>(a, pq, sc, fin, fout, r, 0, smem);
         if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
@@ -1018,7 +1029,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         Flow fin;
         fin.ctl = lf.ctl;
         fin.producers = nq;
-        fin.want = 3 * (HD / 16);
+        fin.want = 3 * (HD / 16) / QS;
         fin.base = base + FL_Q;
         fin.stamp = tl ? tl + 1 : nullptr;
         Flow fout;
@@ -1050,6 +1061,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         if (int(threadIdx.x) >= 64 * po.rg * po.kw) return;
         MMArgs a = oa;
         a.W = P.o;
+        a.tlw = tl;
         a.onorm = P.post_norm;
         Flow fin;
         fin.ctl = lf.ctl;
@@ -1067,7 +1079,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
                 fo.nzero1 = lf.m_d;
             }
         }
-        mm_body<BITS, EPI_RESID, G16, 1, true, true, true, WD>(a, po, sc, fin, fo, r, 0, smem);
+        mm_body<BITS, EPI_RESID, G16, OS, true, true, true, WD>(a, po, sc, fin, fo, r, 0, smem);
         if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
         return;
     }
@@ -1076,6 +1088,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         if (int(threadIdx.x) >= 64 * pg.rg * pg.kw) return;
         MMArgs a = ga;
         a.W = P.gu;
+        a.tlw = tl;
         if (r == 0) {
             // Every o workgroup of this layer has finished waiting.
             fg.zero0 = base + FL_A;
@@ -1090,6 +1103,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     if (int(threadIdx.x) >= 64 * pd.rg * pd.kw) return;
     MMArgs a = da;
     a.W = P.down;
+    a.tlw = tl;
     a.onorm = P.next_norm;
     Flow fout;  // the next layer's q|k|v; after the last layer the head reads x in a later launch
     if (!last) {
@@ -1099,7 +1113,7 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
         fout.mirrors = lf.m_d;
     }
     fg.stamp = tl ? tl + 1 : nullptr;
-    mm_body<BITS, EPI_RESID, G16, DOWN_STRIPS, true, true, true, WD>(a, pd, sc, fg, fout, r, 0, smem);
+    mm_body<BITS, EPI_RESID, G16, DS, true, true, true, WD>(a, pd, sc, fg, fout, r, 0, smem);
     if (tl && threadIdx.x == 0) tl[2] = __builtin_amdgcn_s_memrealtime();
 }
 
@@ -1675,10 +1689,14 @@ int layer_stack_workgroups(int heads, const MMPlan& pq, const MMPlan& po, const 
 const char* layer_stack_unfit(int t, int heads, int kv_heads, int hd, const MMPlan& pq, const MMPlan& po, const MMPlan& pg,
                               const MMPlan& pd) {
     if (t < 1 || t > FTOK || pq.tiles != 1 || po.tiles != 1 || pg.tiles != 1 || pd.tiles != 1) return "the layer stack takes one token tile";
-    if (pq.s != 1 || pq.rg != 1 || pq.nsplit != 1) return "the layer stack needs q|k|v as one workgroup per strip";
-    if (po.s != 1 || po.nsplit != 1) return "the layer stack needs o without a K split";
+    // Strips per wavefront: 1 (q|k|v), 1 (o), DOWN_STRIPS (down) with 128-column K shares; 1, 1, 4
+    // with 256-column shares.
+    const int want_qs = 1, want_ds = pq.wide == 2 ? 4 : DOWN_STRIPS;
+    if (pq.s != want_qs || pq.rg != 1 || pq.nsplit != 1) return "the layer stack needs q|k|v as one row group per workgroup, without a K split";
+    if ((hd / 16) % pq.s) return "q|k|v row blocks must not straddle heads";
+    if (po.s != want_qs || po.nsplit != 1) return "the layer stack needs o without a K split";
     if (pg.nsplit != 1 || pg.s * pg.rg != 2 * GU_STRIPS) return "the layer stack needs gate|up row blocks without a K split";
-    if (pd.s != DOWN_STRIPS) return "the layer stack needs the down plan's strips per wavefront";
+    if (pd.s != want_ds) return "the layer stack needs the down plan's strips per wavefront";
     if (pd.nsplit * FLOW_GU_MIRRORS > FLOW_LAYER_STRIDE - FL_G) return "too many down K splits for the layer counters";
     if (pq.wide != pd.wide || po.wide != pd.wide || pg.wide != pd.wide) return "the layer's plans differ in their K shares";
     if (pd.wide != 1 && hd != 128) return "256-column K shares run in the layer stack for head_dim 128 only";
@@ -1709,9 +1727,9 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
         if (pq.wide == 2) {
             if (g16) throw std::runtime_error("256-column shares need groups of 32 or more");
             switch (qa.W.bits) {
-                case 16: go(k_layers<HD, 16, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
-                case 8: go(k_layers<HD, 8, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
-                default: go(k_layers<HD, 4, false, 2>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+                case 16: go(k_layers<HD, 16, false, 2, 1, 1, 4>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+                case 8: go(k_layers<HD, 8, false, 2, 1, 1, 4>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
+                default: go(k_layers<HD, 4, false, 2, 1, 1, 4>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
             }
             FCHECK(hipGetLastError());
             return;

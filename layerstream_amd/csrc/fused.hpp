@@ -88,6 +88,10 @@ void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, fl
 
 struct MMArgs {
     TMat W;
+    // Layer-stack timeline words of this workgroup (profiling; null: none): 3 its inputs loaded
+    // (wavefront 0), 4 products issued (wavefront 0), 5 row-group sums done, 6 epilogue stores
+    // issued.
+    unsigned long long* tlw = nullptr;
     // input: fragments, tile stride frag_stride; optional RMSNorm (1 / rms from ss partials)
     const uint8_t* frags = nullptr;
     size_t frag_stride = 0;
@@ -270,8 +274,8 @@ struct LayerFlows {
     int layers = 0;
     int gu_per = 1;                      // gate|up row blocks per down K split
     int m_a = 1, m_o = 1, m_d = 1, m_g = 1;  // copies of the attention -> o, o -> gate|up, down -> q|k|v, gate|up -> down counters
-    // Per-workgroup timeline (LS_STACK_TIMELINE=1), [workgroup][4] s_memrealtime counts: entry,
-    // input there (after the wait), done; word 3 is unused.
+    // Per-workgroup timeline (LS_STACK_TIMELINE=1), [workgroup][8] s_memrealtime counts: 0 entry,
+    // 1 input there (after the wait), 2 done, 3-6 matrix roles' phases (MMArgs::tlw), 7 unused.
     unsigned long long* tl = nullptr;
 };
 // Workgroups of one layer in the layer-stack launch.

@@ -701,6 +701,11 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         if (const char* e = std::getenv("LS_WIDE"); e && std::atoi(e) == 0) wide_ = 1;
         kw_qkv_ = kw_o_ = kw_gu_ = kw_down_ = wide_ == 2 ? 8 : 16;
         kw_head_ = 16;
+        // Down in four strips per wavefront: half the workgroups of two (192 for 3B), each reading
+        // its input fragments once for 64 rows; the layer stack's down stage measured 13 us
+        // against 17 us. q|k|v and o stay at one strip per wavefront (four measured slower: 8.5
+        // against 6.7 us, the products of a wavefront's four strips run one after another).
+        if (wide_ == 2 && c.hidden % 64 == 0) ds_ = 4;
     }
     plan_kw_from_env();
     if (const char* e = std::getenv("LS_FUSE")) fuse_on_ = std::atoi(e) != 0;  // fused launches (default on)
@@ -727,8 +732,8 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         const TMat e_res = tile_shape(c.embed_format.bits, c.embed_format.group, int(c.vocab), int(h), 256);
         const int n = int(T);
         const TMat e_chunk = tile_shape(c.embed_format.bits, c.embed_format.group, int(STREAM_HEAD_ROWS), int(h), 256);
-        const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, 1, wide_),  mm_plan(la.o, 1, kw_o_, n, 1, wide_),
-                                gu_plan(la.gu, kw_gu_, n, wide_), mm_plan(la.down, 1, kw_down_, n, DOWN_STRIPS, wide_),
+        const MMPlan plans[] = {mm_plan(la.qkv, 1, kw_qkv_, n, qs_, wide_),  mm_plan(la.o, 1, kw_o_, n, os_, wide_),
+                                gu_plan(la.gu, kw_gu_, n, wide_), mm_plan(la.down, 1, kw_down_, n, ds_, wide_),
                                 mm_plan(e_res, 1, kw_head_, n, 4),       mm_plan(e_chunk, 1, kw_head_, n, 4)};
         size_t pf = 0, nc = 0;
         for (const MMPlan& pl : plans) {
@@ -780,11 +785,11 @@ Model::Model(const Source& src, int mode, int slots, size_t max_ctx, int device,
         // The persistent pass, when its plans fit (the plans of a one-tile pass do not depend on
         // its token count).
         const DevLayer& L0 = prov_->layer(0);
-        const MMPlan pq = mm_plan(L0.qkv, 1, kw_qkv_, 1, 1, wide_), po = mm_plan(L0.o, 1, kw_o_, 1, 1, wide_);
-        const MMPlan pg = gu_plan(L0.gu, kw_gu_, 1, wide_), pd = mm_plan(L0.down, 1, kw_down_, 1, DOWN_STRIPS, wide_);
+        const MMPlan pq = mm_plan(L0.qkv, 1, kw_qkv_, 1, qs_, wide_), po = mm_plan(L0.o, 1, kw_o_, 1, os_, wide_);
+        const MMPlan pg = gu_plan(L0.gu, kw_gu_, 1, wide_), pd = mm_plan(L0.down, 1, kw_down_, 1, ds_, wide_);
         if (const char* e = std::getenv("LS_STACK_TIMELINE"); e && std::atoi(e) != 0 && !layer_stack_unfit(1, int(c.heads), int(c.kv_heads), int(c.head_dim), pq, po, pg, pd)) {
             // Per-workgroup stamps of the layer stack (entry, input there, done), for profiling.
-            stack_tl_ = DevBuf(size_t(c.layers) * layer_stack_workgroups(int(c.heads), pq, po, pg, pd) * 4 * 8);
+            stack_tl_ = DevBuf(size_t(c.layers) * layer_stack_workgroups(int(c.heads), pq, po, pg, pd) * 8 * 8);
             HIPC(hipMemsetAsync(stack_tl_.p, 0, stack_tl_.n, stream_));
         }
         if (const char* e = std::getenv("LS_PASS")) pass_on_ = std::atoi(e) != 0;  // persistent pass (default off)
@@ -954,8 +959,8 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
     if (res && !bv && stack_on_ && fuse_on_ && layer_ptrs_.p) {
         // One launch for every layer: the same plans (so the same bits) as the per-layer
         // launches below.
-        const MMPlan pq = mm_plan(L0->qkv, 1, kw_qkv_, T, 1, wide_), po = mm_plan(L0->o, 1, kw_o_, T, 1, wide_);
-        const MMPlan pg = gu_plan(L0->gu, kw_gu_, T, wide_), pd = mm_plan(L0->down, 1, kw_down_, T, DOWN_STRIPS, wide_);
+        const MMPlan pq = mm_plan(L0->qkv, 1, kw_qkv_, T, qs_, wide_), po = mm_plan(L0->o, 1, kw_o_, T, os_, wide_);
+        const MMPlan pg = gu_plan(L0->gu, kw_gu_, T, wide_), pd = mm_plan(L0->down, 1, kw_down_, T, ds_, wide_);
         if (!layer_stack_unfit(T, heads, kvh, hd, pq, po, pg, pd)) {
             MMArgs qa;
             qa.W = L0->qkv;
@@ -1062,7 +1067,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.kv_heads = kvh;
             a.hd = hd;
         }
-        const MMPlan pq = mm_plan(L.qkv, 1, kw_qkv_, T, 1, wide_);
+        const MMPlan pq = mm_plan(L.qkv, 1, kw_qkv_, T, qs_, wide_);
         {
             MMArgs a;
             a.W = L.o;
@@ -1076,7 +1081,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
             a.onorm = L.post_norm;
             a.oss = ss;
             a.oss_slots = slots_h_;
-            const MMPlan po = mm_plan(L.o, 1, kw_o_, T, 1, wide_);
+            const MMPlan po = mm_plan(L.o, 1, kw_o_, T, os_, wide_);
             // One launch for attention and o when the o workgroups can fetch their weights while
             // attention runs (one token tile, every workgroup resident at once); q|k|v joins it
             // when it runs as one workgroup per strip, and attention then fetches the cached
@@ -1152,7 +1157,7 @@ void Model::forward_chunk(const uint32_t* tok, const uint32_t* dtok, size_t t, s
                 d.pf = N.qkv.data;
                 d.pf_bytes = size_t(end - N.qkv.data);
             }
-            const MMPlan pg = gu_plan(L.gu, kw_gu_, T, wide_), pd = mm_plan(L.down, 1, kw_down_, T, DOWN_STRIPS, wide_);
+            const MMPlan pg = gu_plan(L.gu, kw_gu_, T, wide_), pd = mm_plan(L.down, 1, kw_down_, T, ds_, wide_);
             // Fused only when both roles fit on the device at one workgroup per CU (their
             // wavefronts fill a CU's register file): a down workgroup that started after a
             // gate|up one had finished would fetch its weights late. Either path gives the same
