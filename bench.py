@@ -354,6 +354,8 @@ def main():
     ap.add_argument("--prefill", action="store_true",
                     help="time the prefill of the config's prompt (C2: 512 tokens, C3: 2048) instead of verify steps; "
                     "prints a prefill throughput line with an MFMA roofline")
+    ap.add_argument("--stack-timeline", action="store_true",
+                    help="run the layer stack with per-workgroup stamps (LS_STACK_TIMELINE=1) and print its per-stage timeline")
     ap.add_argument("--stage-timeline", action="store_true",
                     help="run the workload through the persistent layer pass (LS_PASS=1) with its per-unit timeline and print a "
                     "per-stage summary of the last verify step instead of the JSON line")
@@ -383,6 +385,10 @@ def main():
             sys.exit("--stage-timeline takes a single-sequence workload")
         os.environ["LS_PASS"] = "1"
         os.environ["LS_PASS_TIMELINE"] = "1"
+    if args.stack_timeline:
+        if conf["batch"] > 1:
+            sys.exit("--stack-timeline takes a single-sequence workload")
+        os.environ["LS_STACK_TIMELINE"] = "1"
     if args.prefill:
         if conf["batch"] > 1 or conf["prompt"] < 1:
             sys.exit("--prefill takes a single-sequence workload with a prompt")
@@ -462,6 +468,14 @@ def run_single(args, conf):
         if tl is None:
             sys.exit("the persistent layer pass does not fit this model")
         print_stage_timeline(tl, conf, args, wall / K)
+        run.close()
+        drafter.close()
+        return
+    if args.stack_timeline:
+        tl = model.debug_timeline(raw=True)
+        if tl is None:
+            sys.exit("the layer stack does not run this model")
+        print_stack_timeline(tl, conf, args, wall / K)
         run.close()
         drafter.close()
         return
@@ -706,6 +720,50 @@ def print_stage_timeline(tl, conf, args, step_s):
         win = np.nanmax(v[:, 1:9], axis=1)
         cols = [v[:, 13] - v[:, 0], v[:, 1] - v[:, 13], mf - win, v[:, 10] - mf, v[:, 11] - v[:, 10], v[:, 24] - v[:, 11]]
         print("| " + STAGES[s] + " | " + " | ".join("-" if np.all(np.isnan(c)) else f"{np.nanmean(c):.2f}" for c in cols) + " |")
+
+
+def print_stack_timeline(tl, conf, args, step_s):
+    """Per-stage summary of the layer-stack launch's stamps for the last verify step (100 MHz
+    ticks, [workgroup][8]: 0 entry, 1 input there, 2 done, 3 inputs loaded, 4 products issued, 5
+    row-group sums done, 6 epilogue stores issued, 7 layer << 8 | role). Layers 1 .. L-2."""
+    tl = tl.reshape(-1, 8).astype(np.int64)
+    layer, role = tl[:, 7] >> 8, tl[:, 7] & 255
+    L = int(layer.max()) + 1
+    t0 = tl[:, 0][tl[:, 0] > 0].min()
+    t = np.where(tl[:, :7] > 0, (tl[:, :7] - t0) / 100.0, np.nan)
+    span = np.nanmax(t[:, 2])
+    counts = [int(np.sum((layer == 1) & (role == s))) for s in range(5)]
+    print(f"# Layer stack, per-stage timeline ({args.config}: {describe(conf)}, k={conf['k']})\n")
+    print(f"Verify step {step_s * 1e3:.3f} ms on the host clock; stack launch {span:.1f} us, {span / L:.2f} us per layer; "
+          f"workgroups per layer and stage {counts}.\n")
+    print("Per stage, us after the previous stage's last workgroup finished (mean over layers 1..L-2); 'late' is the "
+          "fraction of the stage's workgroups that entered after that point (no earlier weight fetch):\n")
+    print("| stage | first entry | last entry | median input there | last input there | median done | last done | late |")
+    print("|---|---|---|---|---|---|---|---|")
+    for s in range(5):
+        rows = []
+        for l in range(1, L - 1):
+            prev = np.nanmax(t[(layer == l - 1) & (role == 4), 2]) if s == 0 else np.nanmax(t[(layer == l) & (role == s - 1), 2])
+            v = t[(layer == l) & (role == s)]
+            rows.append([np.nanmin(v[:, 0]) - prev, np.nanmax(v[:, 0]) - prev, np.nanmedian(v[:, 1]) - prev, np.nanmax(v[:, 1]) - prev,
+                         np.nanmedian(v[:, 2]) - prev, np.nanmax(v[:, 2]) - prev, float(np.mean(v[:, 0] > prev))])
+        r = np.mean(np.array(rows), axis=0)
+        print("| " + STAGES[s] + " | " + " | ".join(f"{x:.2f}" for x in r) + " |")
+    print("\nPer workgroup, median us between its own stamps (layers 1..L-2; matrix roles):\n")
+    print("| stage | input there to done | to inputs loaded | loaded to products issued | products to row sums | "
+          "row sums to stores issued | stores issued to done |")
+    print("|---|---|---|---|---|---|---|")
+    mid = (layer >= 1) & (layer <= L - 2)
+    for s in range(5):
+        v = t[mid & (role == s)]
+        cells = [np.nanmedian(v[:, 2] - v[:, 1])]
+        if s != 1:
+            for a, b in ((1, 3), (3, 4), (4, 5), (5, 6), (6, 2)):
+                d = v[:, b] - v[:, a]
+                cells.append(np.nanmedian(d) if np.any(~np.isnan(d)) else np.nan)
+        else:
+            cells += [np.nan] * 5
+        print("| " + STAGES[s] + " | " + " | ".join("-" if np.isnan(x) else f"{x:.2f}" for x in cells) + " |")
 
 
 def run_batch(args, conf):

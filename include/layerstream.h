@@ -221,8 +221,9 @@ int ls_model_debug_fail_next(ls_model* m);
  * stages][32]; 0 when there is no timeline. Without the persistent pass, LS_STACK_TIMELINE=1 makes
  * every workgroup of the layer-stack launch record [workgroup][8] stamps: 0 entry, 1 input there
  * (after its wait; 0 when it has none), 2 done, and for the matrix roles 3 inputs loaded, 4 products
- * issued, 5 row-group sums done, 6 epilogue stores issued (7 unused); workgroups in launch order
- * (per layer: q|k|v, attention, o, gate|up, down). */
+ * issued, 5 row-group sums done, 6 epilogue stores issued, 7 layer << 8 | role (0 q|k|v,
+ * 1 attention, 2 o, 3 gate|up, 4 down); workgroups in launch order. Built for int8 weights at
+ * head_dim 64 and 128 (the 0.5B and 3B shapes); other models refuse the timeline. */
 size_t ls_model_debug_timeline(ls_model* m, uint64_t* out, size_t cap);
 /* Debugging hook: a copy of one of the model's device buffers by name ("x", "xf", "ss", "q",
  * "af", "actf", "kcache", "vcache", "pass_area"), up to cap bytes (out may be NULL). Returns the

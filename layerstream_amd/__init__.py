@@ -457,7 +457,7 @@ class Model:
         products done, 24 flag store acknowledged; 0 where a unit did not run or reach a stamp.
         With raw, the words as they are: also the layer stack's [workgroup][4] stamps
         (LS_STACK_TIMELINE=1 at creation: [workgroup][8]: entry, input there, done, inputs loaded,
-        products issued, row-group sums done, epilogue stores issued, unused)."""
+        products issued, row-group sums done, epilogue stores issued, layer << 8 | role)."""
         n = lib().ls_model_debug_timeline(self.h, None, 0)
         if n == 0:
             return None

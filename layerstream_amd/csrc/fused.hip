@@ -394,7 +394,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         }
     }
 
-    if (a.tlw && threadIdx.x == 0) {
+    if (OUT_FLOW && a.tlw && threadIdx.x == 0) {
         __builtin_amdgcn_s_waitcnt(0);
         a.tlw[3] = __builtin_amdgcn_s_memrealtime();
     }
@@ -404,7 +404,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
 #pragma unroll
     for (int c = 0; c < CPW; c++)
         if (c < nch) chunk_mfma<BITS, G16, S, PRE>(W, s0, c0 + c, c0 * Q, (c0 + nch) * Q, &B[c * Q], raw[c], acc, total, scl[PRE ? c : 0]);
-    if (a.tlw && threadIdx.x == 0) a.tlw[4] = __builtin_amdgcn_s_memrealtime();
+    if (OUT_FLOW && a.tlw && threadIdx.x == 0) a.tlw[4] = __builtin_amdgcn_s_memrealtime();
     // Row-group tile: the kw wavefront sums added in wavefront order. Lane l of strip r holds
     // rows 16 r + 4 (l / 16) + i of token l % 16. Wavefront 0 works out 1 / rms (read after the
     // barriers below) while the other wavefronts finish their products.
@@ -438,7 +438,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             for (int i = 0; i < 4; i++) tl[(16 * (S * rgi + r) + 4 * (lane >> 4) + i) * FTOK + (lane & 15)] = total[r][i];
     }
     __syncthreads();
-    if (a.tlw && threadIdx.x == 0) a.tlw[5] = __builtin_amdgcn_s_memrealtime();
+    if (OUT_FLOW && a.tlw && threadIdx.x == 0) a.tlw[5] = __builtin_amdgcn_s_memrealtime();
 
     // Split K: store this piece; the last workgroup of the row block adds all pieces in split
     // order. Pieces move with 128-bit sc1 buffer accesses and the counter with an agent-scope
@@ -516,7 +516,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 else a.vcache[size_t(crow) * kvd + (ref - h - kvd)] = v;
             }
         }
-        if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
+        if (OUT_FLOW && a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
         if constexpr (OUT_FLOW) qkv_signal(fout, rb * S, a.heads, a.kv_heads, a.hd);
     } else if constexpr (EPI == EPI_RESID) {
         if constexpr (XCOH) {
@@ -578,7 +578,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 if (e < rows_wg * FTOK && tok < nt && row < W.rows)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xr[u]), rx, ((ibase + tok) * a.ldo + row) * 4, 0, CPOL_SC1);
             }
-            if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
+            if (OUT_FLOW && a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
             flow_signal(fout, rb);
         }
     } else if constexpr (EPI == EPI_SILU) {
@@ -609,7 +609,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             if constexpr (OUT_FLOW) write_slot_coherent(rof, 0, col / 32, tok + 16 * ((col % 32) / 8), v);
             else write_slot(tf, col / 32, tok + 16 * ((col % 32) / 8), v);
         }
-        if (a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
+        if (OUT_FLOW && a.tlw && threadIdx.x == 0) a.tlw[6] = __builtin_amdgcn_s_memrealtime();
         if constexpr (OUT_FLOW) flow_signal(fout, rb);
     } else {
         // Output head: logits, optional store, per-token best (value, index) of this block.
@@ -973,7 +973,8 @@ __global__ __launch_bounds__(512) void k_qkv_attn_o(MMArgs qa, MMPlan pq, AttnAr
 // FLOW_LAYER_STRIDE apart): q|k|v -> attention one per head, attention -> o, o -> gate|up,
 // gate|up -> down one per down K split, down -> the next layer's q|k|v.
 // QS, OS, DS: strips per wavefront of q|k|v, o and down (WD and the strips: the plans' wide and s).
-template <int HD, int BITS, bool G16, int WD = 1, int QS = 1, int OS = 1, int DS = DOWN_STRIPS>
+// TL: the per-workgroup timeline (LayerFlows::tl) is recorded.
+template <int HD, int BITS, bool G16, int WD = 1, int QS = 1, int OS = 1, int DS = DOWN_STRIPS, bool TL = false>
 __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp, size_t seq_off, MMArgs qa, MMPlan pq, AttnArgs aa,
                                                 MMArgs oa, MMPlan po, MMArgs ga, MMPlan pg, MMArgs da, MMPlan pd, MMScratch sc,
                                                 LayerFlows lf) {
@@ -985,8 +986,13 @@ __global__ __launch_bounds__(512) void k_layers(const LayerPtrs* __restrict__ lp
     const LayerPtrs& P = lp[l];
     const int base = FLOW_COUNTERS + FLOW_LAYER_STRIDE * l;
     const bool last = l + 1 == lf.layers;
-    unsigned long long* tl = lf.tl ? lf.tl + size_t(blockIdx.x) * 8 : nullptr;
-    if (tl && threadIdx.x == 0) tl[0] = __builtin_amdgcn_s_memrealtime();
+    unsigned long long* tl = TL ? lf.tl + size_t(blockIdx.x) * 8 : nullptr;
+    if (tl && threadIdx.x == 0) {
+        tl[0] = __builtin_amdgcn_s_memrealtime();
+        tl[1] = tl[3] = tl[4] = tl[5] = tl[6] = 0;  // stamps this workgroup may not reach (or not wait for)
+        const int rr = int(blockIdx.x) % per_layer;
+        tl[7] = (unsigned long long)(l) << 8 | (rr < nq ? 0 : rr < nq + na ? 1 : rr < nq + na + no ? 2 : rr < nq + na + no + ng ? 3 : 4);
+    }
     if (r < nq) {
         if (int(threadIdx.x) >= 64 * pq.kw) return;
         MMArgs a = qa;
@@ -1481,7 +1487,8 @@ static void launch(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStr
 void mm_qkv(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     if (a.hd % 2 || a.hd / 2 > ROPE_HALF_MAX) throw std::runtime_error("head_dim must be even and at most 256");
     if ((a.heads + a.kv_heads) * a.hd % 16) throw std::runtime_error("q|k rows must fill whole strips");
-    launch<EPI_QKV, 1>(a, p, sc, s);
+    if (p.s == 4) launch<EPI_QKV, 4>(a, p, sc, s);  // 64-row blocks (the epilogue is per row)
+    else launch<EPI_QKV, 1>(a, p, sc, s);
 }
 void mm_residual(const MMArgs& a, const MMPlan& p, const MMScratch& sc, hipStream_t s) {
     switch (p.s) {
@@ -1726,6 +1733,12 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
     if constexpr (HD == 128) {
         if (pq.wide == 2) {
             if (g16) throw std::runtime_error("256-column shares need groups of 32 or more");
+            if (lf.tl) {
+                if (qa.W.bits != 8 || HD != 128) throw std::runtime_error("the layer-stack timeline is built for int8 weights");
+                go(k_layers<HD, 8, false, 2, 1, 1, 4, true>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+                FCHECK(hipGetLastError());
+                return;
+            }
             switch (qa.W.bits) {
                 case 16: go(k_layers<HD, 16, false, 2, 1, 1, 4>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
                 case 8: go(k_layers<HD, 8, false, 2, 1, 1, 4>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
@@ -1736,6 +1749,15 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
         }
     }
     if (pq.wide != 1) throw std::runtime_error("256-column K shares run in the layer stack for head_dim 128 only");
+    if (lf.tl) {
+        if constexpr (HD == 64) {
+            if (qa.W.bits != 8 || g16) throw std::runtime_error("the layer-stack timeline is built for int8 weights in groups of 32 or more");
+            go(k_layers<HD, 8, false, 1, 1, 1, DOWN_STRIPS, true>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf);
+            FCHECK(hipGetLastError());
+            return;
+        }
+        throw std::runtime_error("the layer-stack timeline is built for head_dim 64 and 128");
+    }
     switch (qa.W.bits) {
         case 16: go(k_layers<HD, 16, false>, grid, block, lds, s, lp, seq_off, qa, pq, aa, oa, po, ga, pg, da, pd, sc, lf); break;
         case 8:

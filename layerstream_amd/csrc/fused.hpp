@@ -275,7 +275,8 @@ struct LayerFlows {
     int gu_per = 1;                      // gate|up row blocks per down K split
     int m_a = 1, m_o = 1, m_d = 1, m_g = 1;  // copies of the attention -> o, o -> gate|up, down -> q|k|v, gate|up -> down counters
     // Per-workgroup timeline (LS_STACK_TIMELINE=1), [workgroup][8] s_memrealtime counts: 0 entry,
-    // 1 input there (after the wait), 2 done, 3-6 matrix roles' phases (MMArgs::tlw), 7 unused.
+    // 1 input there (after the wait), 2 done, 3-6 matrix roles' phases (MMArgs::tlw); word 7 is
+    // layer << 8 | role (0 q|k|v, 1 attention, 2 o, 3 gate|up, 4 down).
     unsigned long long* tl = nullptr;
 };
 // Workgroups of one layer in the layer-stack launch.

@@ -218,6 +218,7 @@ private:
     int kw_qkv_ = 7, kw_o_ = 7, kw_gu_ = 7, kw_down_ = 8, kw_head_ = 7;
     int wide_ = 1;  // K share of a wavefront in 128-column units (MMPlan::wide) for every layer matrix
     int qs_ = 1, os_ = 1, ds_ = DOWN_STRIPS;  // strips per wavefront of q|k|v, o and down
+    int mqs_ = 1, mos_ = 1, mds_ = DOWN_STRIPS;  // the same in launches over several token tiles
     hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
     double last_step_ms_ = 0;
     int prof_ = 0;  // profiling mode (set_profiling)
