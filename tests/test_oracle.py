@@ -45,7 +45,7 @@ def test_format_validation():
 
 
 def test_layer_block_sizes():
-    """Layer block sizes of the 0.5B shape (SURVEY a18 figures recomputed from the layout)."""
+    """Layer block sizes of the 0.5B shape, recomputed from the layout (src/weights.rs row sizes)."""
     import ctypes as C
 
     base = dict(hidden=896, inter=4864, layers=24, heads=14, kv_heads=2, head_dim=64, vocab=151936, eps=1e-6, rope_theta=1e6)
