@@ -257,6 +257,14 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         else attn_load<HD>(r, b, last_key, kc, vc, kv, col0, g, c);
     };
     if (first < nb && first < nold) load_block(ba, first);
+    // In a layer-stack launch (IN_FLOW, head_dim up to 64: registers to spare) the wavefront's
+    // second key block of cached keys is requested before the wait too, so long contexts (two
+    // blocks per wavefront from 1024 keys) meet no load after the input arrives.
+    constexpr bool PF2 = IN_FLOW && HD <= 64;
+    AttnBlock<HD> bb;
+    const int second = first + stride;
+    if constexpr (PF2)
+        if (second < nb && second < nold) load_block(bb, second);
     if constexpr (IN_FLOW) {
         flow_wait(fin, head, s);
         if (first < nb && first >= nold) load_block(ba, first);
@@ -319,6 +327,13 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
         }
     };
     for (int b = first; b < nb; b += stride) {
+        if constexpr (PF2) {
+            if (b == second) {
+                if (b >= nold) load_block(bb, b);
+                block(b, bb);
+                continue;
+            }
+        }
         if (b != first) load_block(ba, b);
         block(b, ba);
     }
