@@ -268,3 +268,30 @@ def test_a_failed_in_launch_wait_is_an_error_and_the_next_call_is_clean():
         gm.forward_multi([a, 1, 2], 3)
     assert gm.pos() == p
     assert np.array_equal(bits(gm.forward_multi([a, 1, 2], 3)), bits(ref))
+
+
+def test_c2_full_generation_matches_the_oracle_token_for_token():
+    """The headline workload end to end: 0.5B int8-g64 (clip search), a 512-token prompt of the
+    benchmark's seeded ids, then 256 generated tokens by speculative decoding with k=8 scripted
+    drafts (60% of them the greedy token). Every emitted token equals the oracle's own greedy
+    continuation (src/spec.rs: speculation never changes the output), and so does the GPU's plain
+    greedy decoding; the accepted counts per step come from the device's verify steps."""
+    say("C2: build")
+    m = qwen05b((8, 64))
+    prompt = np.random.default_rng(512).integers(0, 151936, 512).tolist()
+    n = 256
+    say("C2: oracle greedy", n)
+    cpu = cpu_model(m, max_ctx=1024)
+    want = O.plain_greedy(cpu, prompt, n)
+    assert len(want) == n
+    say("C2: gpu greedy")
+    gm = gpu_model(m, max_ctx=1024)
+    got_plain = LS.greedy_generate(gm, prompt, n)
+    assert got_plain == want
+    say("C2: gpu speculative k=8")
+    d = LS.ScriptedDrafter(want, 0.6, 2024, 151936)
+    got, st = LS.speculative_greedy(gpu_model(m, max_ctx=1024), d, prompt, n, 8)
+    d.close()
+    say("C2: stats", st)
+    assert got == want
+    assert st["target_passes"] < n
