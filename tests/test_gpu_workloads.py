@@ -295,3 +295,29 @@ def test_c2_full_generation_matches_the_oracle_token_for_token():
     say("C2: stats", st)
     assert got == want
     assert st["target_passes"] < n
+
+
+def test_c1_and_c3_full_generation_match_the_oracle_token_for_token():
+    """The other single-sequence workloads end to end: 0.5B bf16 after a 64-token prompt with k=4
+    drafts, and 0.5B int4-g32 after a 2048-token prompt with k=8 drafts, resident and streamed from
+    pinned memory through two device slots; 128 generated tokens each, equal to the oracle's greedy
+    continuation token for token."""
+    for name, fmt, n_prompt, k, modes in (("C1", None, 64, 4, ("resident",)), ("C3", (4, 32), 2048, 8, ("resident", "stream"))):
+        say(name, ": build")
+        m = qwen05b(fmt)
+        prompt = np.random.default_rng(512).integers(0, 151936, n_prompt).tolist()
+        n = 128
+        say(name, ": oracle greedy", n)
+        want = O.plain_greedy(cpu_model(m, max_ctx=n_prompt + n + 16), prompt, n)
+        for mode in modes:
+            say(name, ": gpu speculative", mode)
+            if mode == "resident":
+                tm = gpu_model(m, max_ctx=n_prompt + n + 16)
+            else:
+                src = LS.Source.from_lsq_image(np.frombuffer(m["lsq"], np.uint8).copy()).pinned_copy()
+                tm = LS.Model(src, LS.MODE_STREAM, 2, n_prompt + n + 16)
+            d = LS.ScriptedDrafter(want, 0.6, 2024, 151936)
+            got, st = LS.speculative_greedy(tm, d, prompt, n, k)
+            d.close()
+            say(name, mode, "target passes", st["target_passes"])
+            assert got == want, (name, mode)
