@@ -321,3 +321,21 @@ def test_c1_and_c3_full_generation_match_the_oracle_token_for_token():
             d.close()
             say(name, mode, "target passes", st["target_passes"])
             assert got == want, (name, mode)
+
+
+def test_c5_generation_matches_the_oracle_token_for_token():
+    """The 3B workload end to end on a shorter run: int8-g64 after a 1024-token prompt, 32 tokens by
+    speculation with k=8 scripted drafts through the layer stack; every token equals the oracle's
+    greedy continuation."""
+    say("C5 gen: build")
+    m = qwen3b((8, 64))
+    prompt = np.random.default_rng(512).integers(0, 151936, 1024).tolist()
+    n = 32
+    say("C5 gen: oracle greedy", n)
+    want = O.plain_greedy(cpu_model(m, max_ctx=1100), prompt, n)
+    say("C5 gen: gpu speculative")
+    d = LS.ScriptedDrafter(want, 0.6, 2024, 151936)
+    got, st = LS.speculative_greedy(gpu_model(m, max_ctx=1100), d, prompt, n, 8)
+    d.close()
+    say("C5 gen: target passes", st["target_passes"])
+    assert got == want
