@@ -672,11 +672,29 @@ __device__ __forceinline__ void xcd_tile_map(int& bx, int& tile) {
     tile = P % tiles;
 }
 
+// The same for a launch with a K split: each XCD gets a contiguous run of (split, tile, row block)
+// triples, row block innermost, so the row blocks that read one split of one tile's input
+// fragments run side by side on one XCD (the fragments, 96 B per input column and token tile, are
+// what a down launch over 9 tiles mostly fetched: 47 MB per launch for 4.4 MB of weights), and a
+// run covers several tiles of a split, whose weights the L2 then serves again.
+__device__ __forceinline__ void xcd_split_map(int& bx, int& tile, int nsplit) {
+    const int tiles = gridDim.y, G = gridDim.x * tiles, nrb = gridDim.x / nsplit;
+    const int L = blockIdx.x + blockIdx.y * gridDim.x;
+    const int x = L % 8, k = L / 8, base = G / 8, rem = G % 8;
+    const int P = x * base + min(x, rem) + k;
+    const int rb = P % nrb, rest = P / nrb;
+    tile = rest % tiles;
+    bx = rb * nsplit + rest / tiles;
+}
+
 template <int BITS, int EPI, bool G16, int S, int WD = 1>
 __global__ __launch_bounds__((WD > 1 ? 8 : mm_max_waves(BITS, G16 ? 16 : 32, S)) * 64) void k_mm(MMArgs a, MMPlan p, MMScratch sc) {
     extern __shared__ __align__(16) uint8_t smem[];
     int bx = blockIdx.x, tile = blockIdx.y;
-    if (gridDim.y > 1) xcd_tile_map(bx, tile);
+    if (gridDim.y > 1) {
+        if (p.nsplit > 1) xcd_split_map(bx, tile, p.nsplit);
+        else xcd_tile_map(bx, tile);
+    }
     mm_body<BITS, EPI, G16, S, false, false, false, WD>(a, p, sc, Flow{}, Flow{}, bx, tile, smem);
 }
 
