@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "frag_dev.hpp"
 #include "fused.hpp"
@@ -475,9 +476,20 @@ __device__ __forceinline__ void attn_body(const AttnArgs& A, int s, int head, in
 // depend only on its own q), so the bits do not change; the launch has heads / kv_heads times
 // fewer workgroups and reads the cache that many times less.
 // ---------------------------------------------------------------------------------------
-// LDS of a grouped workgroup: attn_body's, then the q of up to AWV x 16 (head, row) pairs [pair][HD].
+// Pair tiles per pass of a grouped workgroup: the wavefronts' states of two tiles sit in LDS at
+// once for head_dim <= 64 (one pair of barriers and one merge pass over all 512 threads for both),
+// one tile above (two tiles' states and the staged q do not fit the LDS).
 template <int HD>
-__host__ __device__ constexpr size_t attn_grp_lds_bytes() { return attn_lds_bytes<HD>() + size_t(AWV) * ATQ * HD * 4; }
+__host__ __device__ constexpr int attn_grp_tiles() { return HD <= 64 ? 2 : 1; }
+// LDS of one pair tile's wavefront states: (max, sum) [AWV][16], outputs [AWV x 16][HD + 4].
+template <int HD>
+__host__ __device__ constexpr size_t attn_grp_slot_bytes() { return size_t(2 * AWV * ATQ + AWV * ATQ * (HD + 4)) * 4; }
+// LDS of a grouped workgroup: attn_grp_tiles slots, the q of up to AWV x 16 (head, row) pairs
+// [pair][HD], then a flag.
+template <int HD>
+__host__ __device__ constexpr size_t attn_grp_lds_bytes() {
+    return attn_grp_tiles<HD>() * attn_grp_slot_bytes<HD>() + size_t(AWV) * ATQ * HD * 4 + 16;
+}
 
 template <int HD>
 __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int grp, int seg, uint8_t* smem) {
@@ -489,12 +501,14 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
     const float* __restrict__ vc = A.vc;
     uint8_t* __restrict__ frags = A.frags;
     const size_t frag_stride = A.frag_stride;
-    constexpr int H4 = HD / 4, DB = HD / 16;
-    float(*sm_m)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem);
-    float(*sm_l)[ATQ] = reinterpret_cast<float(*)[ATQ]>(smem + AWV * ATQ * 4);
-    constexpr int HP = HD + 4;
-    float* sm_o = reinterpret_cast<float*>(smem + 2 * AWV * ATQ * 4);
-    int& flag = *reinterpret_cast<int*>(smem + 2 * AWV * ATQ * 4 + AWV * ATQ * HP * 4);
+    constexpr int H4 = HD / 4, DB = HD / 16, TP = attn_grp_tiles<HD>(), HP = HD + 4;
+    constexpr size_t SLOT = attn_grp_slot_bytes<HD>();
+    // Slot u: (max, sum) of each wavefront and query column, then the wavefronts' outputs.
+    auto sm_m = [&](int u) { return reinterpret_cast<float(*)[ATQ]>(smem + u * SLOT); };
+    auto sm_l = [&](int u) { return reinterpret_cast<float(*)[ATQ]>(smem + u * SLOT + AWV * ATQ * 4); };
+    auto sm_o = [&](int u) { return reinterpret_cast<float*>(smem + u * SLOT + 2 * AWV * ATQ * 4); };
+    float* sq = reinterpret_cast<float*>(smem + TP * SLOT);
+    int& flag = *reinterpret_cast<int*>(smem + TP * SLOT + size_t(AWV) * ATQ * HD * 4);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c = lane & 15, g = lane >> 4;
     const int kv = kv_heads * HD, col0 = grp * HD;
     int i0, nq, pos_first;
@@ -525,8 +539,8 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
     if (one_block) attn_load<HD>(ba, first, last_key, kc, vc, kv, col0, g, c);
     // The group's (head, row) pairs, pair hh nq + i = head grp hpg + hh at row i0 + i, fill the
     // 16 query columns of the MFMAs in tiles of 16 (9-row verify blocks of 7 heads: 4 tiles of
-    // 16, not 7 of 9). Every pair's q into LDS at once (slots past the pairs: zeros).
-    float* sq = reinterpret_cast<float*>(smem + attn_lds_bytes<HD>());
+    // 16, not 7 of 9). Every pair's q into LDS at once (slots past the pairs: zeros): one round
+    // trip to memory for all passes.
     const int npairs = hpg * nq, ptiles = (npairs + ATQ - 1) / ATQ;
     for (int e = tid; e < ptiles * ATQ * (HD / 4); e += AWV * 64) {
         const int pr = e / (HD / 4), d = 4 * (e % (HD / 4));
@@ -535,55 +549,68 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
         *reinterpret_cast<float4*>(sq + pr * HD + d) = x;
     }
     __syncthreads();
-    float qr[H4];
-    for (int pt = 0; pt < ptiles; pt++) {
-        // Query column c: pair pt 16 + c, its row at position pos_first + row.
-        const int pc = pt * ATQ + c;
-        const bool live_c = pc < npairs;
-        const int pos_c = pos_first + pc % nq;
+    // NT pair tiles from pt0: each wavefront's states of them over its blocks in order, then
+    // their merge over the wavefronts in wavefront order (as attn_body), NT tiles per pair of
+    // barriers. The tiles' chains are independent, so their MFMAs interleave.
+    auto pair_tiles = [&](int pt0, auto nt) {
+        constexpr int NT = decltype(nt)::value;
+        float qr[NT][H4], M[NT], Lp[NT];
+        int pos_c[NT];
+        bool live_c[NT];
+        attn_f32x4 O[NT][DB];
 #pragma unroll
-        for (int j = 0; j < H4; j += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(sq + pc * HD + g * H4 + j);
-            qr[j] = x.x;
-            qr[j + 1] = x.y;
-            qr[j + 2] = x.z;
-            qr[j + 3] = x.w;
+        for (int u = 0; u < NT; u++) {
+            // Query column c: pair (pt0 + u) 16 + c, its row at position pos_first + row.
+            const int pc = (pt0 + u) * ATQ + c;
+            live_c[u] = pc < npairs;
+            pos_c[u] = pos_first + pc % nq;
+#pragma unroll
+            for (int j = 0; j < H4; j += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(sq + pc * HD + g * H4 + j);
+                qr[u][j] = x.x;
+                qr[u][j + 1] = x.y;
+                qr[u][j + 2] = x.z;
+                qr[u][j + 3] = x.w;
+            }
+            M[u] = -INFINITY;
+            Lp[u] = 0.0f;
+#pragma unroll
+            for (int db = 0; db < DB; db++) O[u][db] = attn_f32x4{0, 0, 0, 0};
         }
-        float M = -INFINITY, Lp = 0.0f;
-        attn_f32x4 O[DB];
-#pragma unroll
-        for (int db = 0; db < DB; db++) O[db] = attn_f32x4{0, 0, 0, 0};
         auto block = [&](int b, const AttnBlock<HD>& r) {
-            attn_f32x4 sc = {0, 0, 0, 0};
 #pragma unroll
-            for (int j = 0; j < H4; j++) sc = mfma_f32(r.k[j], qr[j], sc);
-            float sv[4];
-            float mx = -INFINITY;
+            for (int u = 0; u < NT; u++) {
+                attn_f32x4 sc = {0, 0, 0, 0};
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int key = AKB * b + 4 * g + i;
-                sv[i] = (live_c && key <= pos_c) ? sc[i] * scale : -INFINITY;
-                mx = fmaxf(mx, sv[i]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float Mn = fmaxf(M, mx);
-            const float corr = M == -INFINITY ? 0.0f : expf(M - Mn);
-            float p[4], ls = 0.0f;
+                for (int j = 0; j < H4; j++) sc = mfma_f32(r.k[j], qr[u][j], sc);
+                float sv[4];
+                float mx = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                p[i] = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
-                ls += p[i];
-            }
-            Lp = __builtin_fmaf(Lp, corr, ls);
-            M = Mn;
+                for (int i = 0; i < 4; i++) {
+                    const int key = AKB * b + 4 * g + i;
+                    sv[i] = (live_c[u] && key <= pos_c[u]) ? sc[i] * scale : -INFINITY;
+                    mx = fmaxf(mx, sv[i]);
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                const float Mn = fmaxf(M[u], mx);
+                const float corr = M[u] == -INFINITY ? 0.0f : expf(M[u] - Mn);
+                float p[4], ls = 0.0f;
 #pragma unroll
-            for (int db = 0; db < DB; db++) {
-                attn_f32x4 acc = {0, 0, 0, 0};
+                for (int i = 0; i < 4; i++) {
+                    p[i] = sv[i] == -INFINITY ? 0.0f : expf(sv[i] - Mn);
+                    ls += p[i];
+                }
+                Lp[u] = __builtin_fmaf(Lp[u], corr, ls);
+                M[u] = Mn;
 #pragma unroll
-                for (int u = 0; u < 4; u++) acc = mfma_f32(r.v[u * DB + db], p[u], acc);
+                for (int db = 0; db < DB; db++) {
+                    attn_f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int i = 0; i < 4; i++) O[db][i] = __builtin_fmaf(O[db][i], corr, acc[i]);
+                    for (int k = 0; k < 4; k++) acc = mfma_f32(r.v[k * DB + db], p[k], acc);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) O[u][db][i] = __builtin_fmaf(O[u][db][i], corr, acc[i]);
+                }
             }
         };
         if (one_block) {
@@ -595,33 +622,36 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
                 block(b, r);
             }
         }
-        // The wavefronts' states of these pairs, merged in wavefront order (as attn_body).
-        float L = Lp + __shfl_xor(Lp, 16, 64);
-        L += __shfl_xor(L, 32, 64);
-        if (g == 0) {
-            sm_m[w][c] = M;
-            sm_l[w][c] = L;
-        }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float* dst = &sm_o[(w * ATQ + c) * HP + DB * (4 * g + i)];
-            if constexpr (DB % 4 == 0) {
+        for (int u = 0; u < NT; u++) {
+            float L = Lp[u] + __shfl_xor(Lp[u], 16, 64);
+            L += __shfl_xor(L, 32, 64);
+            if (g == 0) {
+                sm_m(u)[w][c] = M[u];
+                sm_l(u)[w][c] = L;
+            }
 #pragma unroll
-                for (int db = 0; db < DB; db += 4)
-                    *reinterpret_cast<attn_f32x4*>(dst + db) = attn_f32x4{O[db][i], O[db + 1][i], O[db + 2][i], O[db + 3][i]};
-            } else {
+            for (int i = 0; i < 4; i++) {
+                float* dst = &sm_o(u)[(w * ATQ + c) * HP + DB * (4 * g + i)];
+                if constexpr (DB % 4 == 0) {
 #pragma unroll
-                for (int db = 0; db < DB; db++) dst[db] = O[db][i];
+                    for (int db = 0; db < DB; db += 4)
+                        *reinterpret_cast<attn_f32x4*>(dst + db) = attn_f32x4{O[u][db][i], O[u][db + 1][i], O[u][db + 2][i], O[u][db + 3][i]};
+                } else {
+#pragma unroll
+                    for (int db = 0; db < DB; db++) dst[db] = O[u][db][i];
+                }
             }
         }
         __syncthreads();
-        for (int e = tid; e < ATQ * (HD / 4); e += AWV * 64) {
-            const int tk = e % ATQ, d = 4 * (e / ATQ), pr = pt * ATQ + tk;
+        for (int e = tid; e < NT * ATQ * (HD / 4); e += AWV * 64) {
+            const int u = e / (ATQ * (HD / 4)), f = e % (ATQ * (HD / 4));
+            const int tk = f % ATQ, d = 4 * (f / ATQ), pr = (pt0 + u) * ATQ + tk;
             if (pr >= npairs) continue;
             float mw[AWV], Mx = -INFINITY;
 #pragma unroll
             for (int k = 0; k < AWV; k++) {
-                mw[k] = sm_m[k][tk];
+                mw[k] = sm_m(u)[k][tk];
                 Mx = fmaxf(Mx, mw[k]);
             }
             float Lw = 0.0f;
@@ -629,8 +659,8 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
 #pragma unroll
             for (int k = 0; k < AWV; k++) {
                 const float e2 = mw[k] == -INFINITY ? 0.0f : expf(mw[k] - Mx);
-                Lw = __builtin_fmaf(sm_l[k][tk], e2, Lw);
-                const attn_f32x4 x = *reinterpret_cast<const attn_f32x4*>(&sm_o[(k * ATQ + tk) * HP + d]);
+                Lw = __builtin_fmaf(sm_l(u)[k][tk], e2, Lw);
+                const attn_f32x4 x = *reinterpret_cast<const attn_f32x4*>(&sm_o(u)[(k * ATQ + tk) * HP + d]);
 #pragma unroll
                 for (int i = 0; i < 4; i++) ow[i] = __builtin_fmaf(x[i], e2, ow[i]);
             }
@@ -641,8 +671,12 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
             }
             st_attn_f32x4(ow, ro, int((row * HD + d) * 4));
         }
-        __syncthreads();  // before the next pair tile reuses the LDS
-    }
+        __syncthreads();  // before the next pass reuses the LDS
+    };
+    int pt = 0;
+    for (; pt + TP <= ptiles; pt += TP) pair_tiles(pt, std::integral_constant<int, TP>{});
+    if constexpr (TP > 1)
+        if (pt < ptiles) pair_tiles(pt, std::integral_constant<int, 1>{});
 
     // The last workgroup of (group, segment) merges the ASPLIT states of every pair in order.
     __builtin_amdgcn_s_waitcnt(0);
@@ -659,7 +693,7 @@ __device__ __forceinline__ void attn_group_body(const AttnArgs& A, int s, int gr
     // (head, token) pairs over the 32 row slots of the workgroup, every head's rows into LDS
     // ([pair][HD]: at most heads_per_group x 16 rows), then the fragments.
     constexpr int DPT = HD / 16;
-    float* Os = sm_o;
+    float* Os = sm_o(0);
     const int sub = tid & 15;
     for (int pr = tid >> 4; pr < hpg * nq; pr += AWV * 64 / 16) {
         const int hh = pr / nq, row = pr % nq, head = grp * hpg + hh;

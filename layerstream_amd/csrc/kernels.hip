@@ -30,7 +30,7 @@ __global__ __launch_bounds__(AWV * 64) void k_attn(AttnArgs a) {
 }
 
 template <int HD>
-__global__ __launch_bounds__(AWV * 64, HD <= 64 ? 4 : 2) void k_attn_grp(AttnArgs a) {  // head_dim <= 64: two workgroups per CU
+__global__ __launch_bounds__(AWV * 64, 2) void k_attn_grp(AttnArgs a) {  // one workgroup per CU (LDS)
     __shared__ __align__(16) uint8_t smem[attn_grp_lds_bytes<HD>()];
     attn_group_body<HD>(a, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }

@@ -13,7 +13,7 @@ import pytest
 import layerstream_amd as LS
 import oracle_py as O
 import tinymodels as T
-from test_gpu import bits, cpu_model, gpu_model, qwen05b, tiny
+from test_gpu import bits, cpu_model, gpu_model, qwen05b, qwen3b, tiny
 
 pytestmark = pytest.mark.gpu
 
@@ -125,15 +125,13 @@ def test_batched_verify_rejects_bad_requests():
         assert b.pos() == 3 + acc + 1, s
 
 
-def test_qwen05b_int8_batched_verify_matches_each_sequence_alone():
-    """The 0.5B shape: a batch of 4 x 9 rows runs the multi-tile kernels (split gate|up and down
-    launches, head over 3 tiles); each sequence alone runs the single-tile fused ones."""
-    q = qwen05b((8, 64))
+def batch_vs_alone(q, vocab, lens, max_ctx, plan, tag, seed=7):
+    """Prompts of the given lengths through one batch model and one model per sequence, then the
+    plan's verify steps (per step, per sequence: drafts from the greedy continuation accepted);
+    every sequence of the batch must give what it gives alone, bit for bit."""
     src = LS.Source.from_lsq_image(q["lsq"])
-    rng = np.random.default_rng(7)
-    lens = [130, 37, 300, 64]
-    prompts = [rng.integers(0, LS.QWEN2_05B["vocab"], n).tolist() for n in lens]
-    max_ctx = 400
+    rng = np.random.default_rng(seed)
+    prompts = [rng.integers(0, vocab, n).tolist() for n in lens]
     batch = LS.Model(src, LS.MODE_RESIDENT, 2, max_ctx, 0, n_seq=len(prompts))
     alone = [LS.Model(src, LS.MODE_RESIDENT, 2, max_ctx, 0) for _ in prompts]
     last = []
@@ -152,13 +150,13 @@ def test_qwen05b_int8_batched_verify_matches_each_sequence_alone():
         alone[s].truncate(p0)
         greedy.append(g)
     done = [1] * len(prompts)
-    for step, goods in enumerate([[8, 0, 3, 5], [2, 8, 0, 1], [0, 0, 8, 8]]):
+    for step, goods in enumerate(plan):
         blocks = []
         for s, good in enumerate(goods):
             g = greedy[s]
-            d = list(g[done[s] : done[s] + good]) + [(g[done[s] + good] + 1) % LS.QWEN2_05B["vocab"]] * (8 - good)
+            d = list(g[done[s] : done[s] + good]) + [(g[done[s] + good] + 1) % vocab] * (8 - good)
             blocks.append([last[s]] + d[:8])
-        say("0.5B batch step", step)
+        say(tag, "batch step", step)
         got = batch.verify_greedy_batch(blocks)
         for s in range(len(prompts)):
             want = alone[s].verify_greedy(blocks[s])
@@ -172,3 +170,19 @@ def test_qwen05b_int8_batched_verify_matches_each_sequence_alone():
         assert batch.pos() == alone[s].pos()
         lb, la = batch.forward([last[s]]), alone[s].forward([last[s]])
         assert np.array_equal(bits(lb), bits(la)), s
+
+
+def test_qwen05b_int8_batched_verify_matches_each_sequence_alone():
+    """The 0.5B shape: a batch of 4 x 9 rows runs the multi-tile kernels (split gate|up and down
+    launches, head over 3 tiles, attention per KV group: 7 heads x 9 rows in 4 query tiles);
+    each sequence alone runs the single-tile fused ones."""
+    q = qwen05b((8, 64))
+    batch_vs_alone(q, LS.QWEN2_05B["vocab"], [130, 37, 300, 64], 400, [[8, 0, 3, 5], [2, 8, 0, 1], [0, 0, 8, 8]], "0.5B")
+
+
+def test_qwen3b_int8_batched_verify_matches_each_sequence_alone():
+    """The 3B shape (head_dim 128, 8 heads per KV group: 72 (head, row) pairs in 5 query tiles,
+    256-column K shares): a batch of 3 x 9 rows against each sequence alone in the layer stack."""
+    say("3B batch: synth + quantize")
+    q = qwen3b((8, 64))
+    batch_vs_alone(q, LS.QWEN2_3B["vocab"], [70, 260, 17], 320, [[8, 0, 3], [2, 8, 0]], "3B")
