@@ -247,7 +247,7 @@ void x_frags(const float* x, int n, int cols, const float* w, uint8_t* frags, fl
 // Dynamic LDS: [wavefront sums (kw > 1)] [tile: 16 S rg rows x 16 floats] [16 inverse rms]
 // [flag] [argmax scratch 2 x 256] [epilogue operands staged by the prologue: residual rows
 // 16 S rg x 16, per-row vector 16 S rg, RoPE cos and sin 2 x 16 x half, per-token position and
-// cache row 2 x 16] [sum-of-squares partials of an in-launch normalised input: rms_stage_bytes].
+// cache row 2 x 16].
 // One matrix workgroup (row block bx / nsplit, K range bx % nsplit, token tile `tile`). With
 // IN_FLOW the input (fragments, and the sum-of-squares partials of a normalised input) comes
 // from earlier workgroups of the same launch: it is read through the coherent path after
@@ -280,7 +280,6 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
     float* rcos = vec + rows_wg;
     float* rsin = rcos + FTOK * (EPI == EPI_QKV ? a.hd / 2 : 0);
     int* tpos = reinterpret_cast<int*>(rsin + FTOK * (EPI == EPI_QKV ? a.hd / 2 : 0));  // [position][cache row] per token
-    float* rst = reinterpret_cast<float*>(tpos + 2 * FTOK);
     const int ibase = tile * FTOK;  // launch token index of token 0 of the tile
 
     // Every load of the wavefront's share (weights, their group scales, and the input when it
@@ -311,12 +310,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             }
         }
     }
-    // Sum-of-squares partials for 1 / rms (wavefront 0), in flight with the weights (with an
-    // in-launch input: after the wait; for 256-column shares, whose weights and fragments fill
-    // the registers, straight into LDS: held in registers across the products they spilled, 41
-    // registers of the 3B int8 layer stack. Elsewhere the LDS path measured slower: 0.5B int8
-    // stack 745 against 720 us).
-    constexpr bool RMS_LDS = IN_FLOW && WD > 1;
+    // Sum-of-squares partials for 1 / rms (wavefront 0), in flight with the weights.
     RmsLoads rms;
     const bool do_rms = a.ss && wv == 0;
     if (do_rms && !IN_FLOW) rms_issue(a, tile, rms);
@@ -371,10 +365,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
                 if (off + size_t(lane) * 16 + 16 <= end) __builtin_amdgcn_global_load_lds(a.pf + off + lane * 16, lds, 16, 0, 0);
         }
         flow_wait(fin, sp, rb);
-        if (do_rms) {
-            if constexpr (RMS_LDS) rms_stage(a, tile, rst);
-            else rms_issue<true>(a, tile, rms);
-        }
+        if (do_rms) rms_issue<true>(a, tile, rms);
         if constexpr (XCOH) {
             const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, a.n * a.ldo * 4, BUF_DWORD3);
 #pragma unroll
@@ -421,10 +412,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
         f32x4* red = reinterpret_cast<f32x4*>(smem);
 #pragma unroll
         for (int r = 0; r < S; r++) red[(wv * S + r) * 64 + lane] = total[r];
-        if (do_rms) {
-            if constexpr (RMS_LDS) rms_finish_staged(a, W.cols, rst, inv);
-            else rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
-        }
+        if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
         __syncthreads();
         for (int e = threadIdx.x; e < p.rg * S * 64; e += nthr) {
             const int g = e / (S * 64), r = (e / 64) % S, ln = e % 64;
@@ -443,10 +431,7 @@ __device__ __forceinline__ void mm_body(const MMArgs& a, const MMPlan& p, const 
             for (int i = 0; i < 4; i++) tl[(16 * (S * g + r) + 4 * (ln >> 4) + i) * FTOK + (ln & 15)] = sum[i];
         }
     } else {
-        if (do_rms) {
-            if constexpr (RMS_LDS) rms_finish_staged(a, W.cols, rst, inv);
-            else rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
-        }
+        if (do_rms) rms_finish<IN_FLOW>(a, tile, W.cols, rms, inv);
 #pragma unroll
         for (int r = 0; r < S; r++)
 #pragma unroll
@@ -1760,8 +1745,7 @@ static void launch_layers(const LayerPtrs* lp, int layers, size_t seq_off, const
     // One workgroup per CU (the launch asks for more than half its LDS): a pass is bound by
     // handoff latency, and twice the resident workgroups poll twice as much (0.5B int8: 0.89 ms
     // per step at one, 0.97 at two; int4: 1.01 and 1.18).
-    const size_t stage = pq.wide > 1 ? rms_stage_bytes(qa.ss_slots) : 0;  // the normalised inputs' partials (q|k|v, gate|up)
-    const size_t lds = std::max({lds_bytes(pq, qa.hd) + stage, lds_bytes(po), lds_bytes(pg) + stage, lds_bytes(pd), attn_lds_bytes<HD>(),
+    const size_t lds = std::max({lds_bytes(pq, qa.hd), lds_bytes(po), lds_bytes(pg), lds_bytes(pd), attn_lds_bytes<HD>(),
                                  size_t(96) << 10});
     const bool g16 = qa.W.bits != 16 && qa.W.group == 16;
     if constexpr (HD == 128) {

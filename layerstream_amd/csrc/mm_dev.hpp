@@ -242,38 +242,6 @@ __device__ __forceinline__ void rms_finish(const MMArgs& a, int tile, int cols, 
     v += __shfl_xor(v, 32, 64);
     if (lane < FTOK) inv[lane] = 1.0f / sqrtf(v / float(cols) + a.eps);
 }
-// LDS that rms_stage fills: 64 floats for every 4 slots.
-__host__ __device__ constexpr size_t rms_stage_bytes(int slots) { return size_t(slots + 3) / 4 * 256; }
-// The sum-of-squares partials of a tile written earlier in the same launch, loaded through the
-// coherent path straight into LDS (no registers held while the products run): load k brings
-// slot part + 4 k of token tok for lane (tok, part) to rst[64 k + lane]; past the last slot it
-// brings the last slot again, which is never added.
-__device__ __forceinline__ void rms_stage(const MMArgs& a, int tile, float* rst) {
-    const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4;
-    const float* base = a.ss + size_t(tile) * a.ss_slots * FTOK;
-    for (int k = 0; k < (a.ss_slots + 3) / 4; k++) {
-        const int sl = min(part + 4 * k, a.ss_slots - 1);
-        __builtin_amdgcn_global_load_lds(base + sl * FTOK + tok, (__attribute__((address_space(3))) void*)(rst + 64 * k), 4, 0, CPOL_SC1);
-    }
-}
-// rms_finish over the partials rms_stage brought: the same additions in the same order.
-__device__ __forceinline__ void rms_finish_staged(const MMArgs& a, int cols, const float* rst, float* inv) {
-    __builtin_amdgcn_s_waitcnt(0);  // the LDS-direct loads have landed
-    asm volatile("" ::: "memory");
-    const int lane = threadIdx.x & 63, tok = lane & 15, part = lane >> 4, nk = (a.ss_slots + 3) / 4;
-    float v = 0.0f;
-    for (int k0 = 0; k0 < nk; k0 += 16) {
-        float x[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) x[k] = k0 + k < nk ? rst[64 * (k0 + k) + lane] : 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; k++) v += part + 4 * (k0 + k) < a.ss_slots ? x[k] : 0.0f;
-    }
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (lane < FTOK) inv[lane] = 1.0f / sqrtf(v / float(cols) + a.eps);
-    (void)tok;
-}
 __device__ __forceinline__ void inv_rms(const MMArgs& a, int tile, int cols, float* inv) {
     RmsLoads r;
     rms_issue(a, tile, r);
